@@ -1,0 +1,148 @@
+/*
+ * wan_attn.h — C ABI of the MI355X (gfx950) attention path of the
+ * Wan2.2-TI2V-5B DiT: flash self-attention, cross-attention with per-sample
+ * key lengths, QK-RMSNorm and 3D-RoPE (standalone and fused into the
+ * attention kernels).
+ *
+ * Conventions
+ *   - Tensors are bf16 device pointers in the DiT projection layout
+ *     [batch, token, head, head_dim] (a view of [batch, token, dim]) described
+ *     by wan_tensor: element strides of batch, token and head; head_dim is
+ *     contiguous.  head_dim must be 128, the data pointer 16-byte aligned and
+ *     every stride a multiple of 8 elements.
+ *   - RoPE tables are fp32 [seqlen, head_dim/2] cos and sin (the layout of
+ *     _rope_tables, models/fast_dit.py:548-558, without the unit dims).
+ *   - Outputs and workspaces are allocated by the caller; the library never
+ *     allocates or frees device memory and never synchronises the stream.
+ *   - `stream` is a hipStream_t (NULL = the null stream).  Every call is
+ *     asynchronous and re-entrant.
+ *   - Return value: WAN_OK or an error code; wan_attn_last_error() returns the
+ *     calling thread's last message.
+ */
+#ifndef WAN_ATTN_H
+#define WAN_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum wan_status {
+  WAN_OK = 0,
+  WAN_ERR_INVALID = 1,     /* bad pointer, shape, stride or length */
+  WAN_ERR_UNSUPPORTED = 2, /* valid but outside what the kernels implement (head_dim != 128, ...) */
+  WAN_ERR_WORKSPACE = 3,   /* workspace missing or too small */
+  WAN_ERR_LAUNCH = 4       /* the HIP runtime rejected a launch */
+};
+
+/* A [batch, token, head, head_dim] bf16 device tensor. */
+typedef struct wan_tensor {
+  void* data;
+  int64_t batch_stride;
+  int64_t token_stride;
+  int64_t head_stride;
+} wan_tensor;
+
+/* Message of the calling thread's last failed call ("" if none). */
+const char* wan_attn_last_error(void);
+
+/* ABI version of this header (incremented on incompatible changes). */
+int wan_attn_abi_version(void);
+
+/*
+ * Self-attention, out = softmax(q k^T * softmax_scale) v over the first
+ * actual_seqlen_k keys (actual_seqlen_k <= 0 means all seqlen_k keys).
+ * Replaces wan_flash_self_attn, kernels/self_attention_nst.py:49-117, and the
+ * _sdpa / _nki_self backends, models/fast_dit.py:186-207, without their
+ * permute/pad copies: q [B, Lq, H, 128], k/v [B, Lk, H, 128] -> out [B, Lq, H, 128].
+ */
+int wan_flash_self_attn(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor out,
+                        int batch, int heads, int seqlen_q, int seqlen_k, int head_dim,
+                        float softmax_scale, int actual_seqlen_k, void* stream);
+
+/*
+ * Cross-attention over text keys with per-sample key lengths:
+ * out[b] = softmax(q[b] k[b, :len_b]^T * scale) v[b, :len_b], len_b =
+ * seqlen_k_dev[b] (device int32 [batch], clamped to [0, seqlen_k]; a sample
+ * with len 0 gets zeros).  seqlen_k_dev == NULL attends to all seqlen_k keys,
+ * as the reference kernel does.
+ * Replaces wan_cross_attn, kernels/cross_attention.py:17-123, and _nki_cross,
+ * models/fast_dit.py:244-255.
+ */
+int wan_cross_attn(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor out,
+                   int batch, int heads, int seqlen_q, int seqlen_k, int head_dim,
+                   float softmax_scale, const int32_t* seqlen_k_dev, void* stream);
+
+/*
+ * Fused self-attention span of _FastBlock.forward, models/fast_dit.py:281-292:
+ *   q,k = _tp_rms_qk(q, k) (RMS over all heads*128 channels of a token, eps,
+ *         bf16 gamma [heads*128]); q,k = _rope(q), _rope(k); out = attention(q, k, v).
+ * q, k, v are the raw projections [B, L, H, 128].  The per-token RMS of q and
+ * the normalised, rotated k are written to `workspace` (at least
+ * wan_self_attn_fused_workspace() bytes, 256-byte aligned); q is normalised
+ * and rotated inside the attention kernel as it is loaded.
+ */
+size_t wan_self_attn_fused_workspace(int batch, int heads, int seqlen);
+int wan_self_attn_fused(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor out,
+                        int batch, int heads, int seqlen, int head_dim,
+                        const void* gamma_q, const void* gamma_k, float eps,
+                        const float* rope_cos, const float* rope_sin, float softmax_scale,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Fused cross-attention span, models/fast_dit.py:297-304:
+ *   q = _tp_rms(q, norm_q); out = cross attention(q, k, v) with per-sample key
+ * lengths as wan_cross_attn.  k is the per-prompt normalised cross K
+ * (_FastCrossKV, models/fast_dit.py:464-477).  Workspace holds the per-token
+ * RMS of q (at least wan_cross_attn_fused_workspace() bytes).
+ */
+size_t wan_cross_attn_fused_workspace(int batch, int heads, int seqlen_q);
+int wan_cross_attn_fused(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor out,
+                         int batch, int heads, int seqlen_q, int seqlen_k, int head_dim,
+                         const void* gamma_q, float eps, float softmax_scale,
+                         const int32_t* seqlen_k_dev,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * 3D-RoPE interleaved-pair rotation in fp32 with one bf16 rounding:
+ * out [B, L, H, 128] contiguous.  Semantics of _rope, models/fast_dit.py:163-169
+ * (the named kernel causal_rope_rotation, kernels/rope.py:39-71, computes the
+ * same rotation from an expanded cos / signed-sin table).
+ */
+int wan_rope(wan_tensor x, void* out, int batch, int seqlen, int heads, int head_dim,
+             const float* rope_cos, const float* rope_sin, void* stream);
+
+/*
+ * RMSNorm over all heads*128 channels of each token with bf16 gamma, the
+ * reference's rounding, optionally followed by the 3D-RoPE rotation:
+ *   out = rope(bf16(bf16(x * rsqrt(mean(x^2) + eps)) * gamma))
+ * _tp_rms at TP=1, models/fast_dit.py:156-160 (on q and k it is _tp_rms_qk,
+ * :134-147; with rope_cos/rope_sin it is the K side of :281-284).  out:
+ * [B, L, H, 128] contiguous, may be NULL when only inv_rms_out (fp32 [B*L],
+ * may be NULL) is wanted; rope_cos/rope_sin may be NULL (no rotation).
+ */
+int wan_rms_norm(wan_tensor x, void* out, int batch, int seqlen, int heads, int head_dim,
+                 const void* gamma, float eps, const float* rope_cos, const float* rope_sin,
+                 float* inv_rms_out, void* stream);
+
+/*
+ * Attention whose query is normalised inside the kernel as it is loaded:
+ *   q' = rope?(bf16(bf16(q * inv_rms_q[b, i]) * gamma_q)),  out = softmax(q' k^T * scale) v
+ * with inv_rms_q from wan_rms_norm (fp32 [B*Lq]).  rope_cos/rope_sin NULL: no
+ * rotation (the cross-attention query, models/fast_dit.py:297-298); non-NULL:
+ * the self-attention query (:281-283), tables of seqlen_q rows.  seqlen_k_dev
+ * as in wan_cross_attn.  This is the kernel behind the two fused entry points.
+ */
+int wan_flash_attn_qnorm(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor out,
+                         int batch, int heads, int seqlen_q, int seqlen_k, int head_dim,
+                         const float* inv_rms_q, const void* gamma_q,
+                         const float* rope_cos, const float* rope_sin, float softmax_scale,
+                         const int32_t* seqlen_k_dev, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WAN_ATTN_H */

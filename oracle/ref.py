@@ -1,0 +1,214 @@
+"""CPU oracle of the Wan DiT attention path — TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
+this module, and only as the checker (or, for the CPU baseline, as the thing
+timed on host cores).  The product path (wan2-ti2v-5b_amd) never calls it.
+
+It restates, in plain torch-on-CPU (and numpy for the brute-force forms), the
+reference's arithmetic for this path, with the reference's bf16 rounding points
+when given bf16 tensors and without them when given fp32 tensors:
+
+  rope_params        wan/modules/rope_neuron.py:14-24
+  wan_freqs          wan/modules/model.py:396-403
+  rope_tables        models/fast_dit.py:548-558
+  rope               models/fast_dit.py:163-169
+  rope_expanded      kernels/rope.py:39-71 (cos_expanded / sin_signed form)
+  rms_qk             models/fast_dit.py:134-147 (TP=1: the all-reduce is the identity, :90-92)
+  rms                models/fast_dit.py:156-160
+  sdpa               models/fast_dit.py:186-189, keys limited to actual_seqlen_k as
+                     kernels/self_attention_nst.py:73-78,715-722
+  self_attn_path     models/fast_dit.py:281-292
+  cross_attn_path    models/fast_dit.py:297-304
+  brute_attention    scripts/validate/attn_bench.py:54-60 (per-head loop), float64 numpy
+
+Each function is pinned by tests/test_oracle.py (closed forms, invariants,
+library routines and float64 brute force); see that file's header.
+"""
+import math
+from typing import Optional, Sequence
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+HEAD_DIM = 128
+DIM = 3072
+NUM_HEADS = 24
+EPS = 1e-6
+THETA = 10000.0
+
+
+# ---------------------------------------------------------------------------
+# RoPE
+# ---------------------------------------------------------------------------
+
+def rope_params(max_seq_len: int, dim: int, theta: float = THETA) -> torch.Tensor:
+    """Angles [max_seq_len, dim//2] fp32: p * theta^(-2j/dim) (wan/modules/rope_neuron.py:14-24)."""
+    return torch.outer(torch.arange(max_seq_len).float(),
+                       1.0 / torch.pow(theta, torch.arange(0, dim, 2).float().div(dim)))
+
+
+def wan_freqs(head_dim: int = HEAD_DIM, max_seq_len: int = 1024) -> torch.Tensor:
+    """Frame/height/width angle table [1024, 64] (wan/modules/model.py:396-403): 44/42/42 dims."""
+    d = head_dim
+    return torch.cat([rope_params(max_seq_len, d - 4 * (d // 6)),
+                      rope_params(max_seq_len, 2 * (d // 6)),
+                      rope_params(max_seq_len, 2 * (d // 6))], dim=1)
+
+
+def rope_tables(freqs: torch.Tensor, grid: Sequence[int], head_dim: int = HEAD_DIM):
+    """cos, sin [L, head_dim/2] fp32 for token index f*h*w + y*w + x (models/fast_dit.py:548-558)."""
+    f, h, w = grid
+    c = head_dim // 2
+    fr = freqs.float().split([c - 2 * (c // 3), c // 3, c // 3], dim=1)
+    ang = torch.cat([
+        fr[0][:f].view(f, 1, 1, -1).expand(f, h, w, -1),
+        fr[1][:h].view(1, h, 1, -1).expand(f, h, w, -1),
+        fr[2][:w].view(1, 1, w, -1).expand(f, h, w, -1),
+    ], dim=-1).reshape(f * h * w, c)
+    return torch.cos(ang), torch.sin(ang)
+
+
+def rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Interleaved-pair rotation, fp32 math, cast back to x.dtype (models/fast_dit.py:163-169).
+
+    x [B, L, n, d]; cos/sin [L, d/2].
+    """
+    B, L, n, d = x.shape
+    cos = cos.view(1, L, 1, d // 2)
+    sin = sin.view(1, L, 1, d // 2)
+    xp = x.float().reshape(B, L, n, d // 2, 2)
+    xr, xi = xp[..., 0], xp[..., 1]
+    out = torch.stack([xr * cos - xi * sin, xr * sin + xi * cos], dim=-1)
+    return out.reshape(B, L, n, d).to(x.dtype)
+
+
+def rope_expanded(x: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
+    """kernels/rope.py:39-71 form in float64: out = x*cos_exp + swap_pairs(x)*sin_signed.
+
+    cos_exp[:, 2j] = cos_exp[:, 2j+1] = cos_j; sin_signed[:, 2j] = -sin_j, [:, 2j+1] = +sin_j
+    (the table layout built by kernels/kernel_builder/rope.py:18-22).  x [L, n, d].
+    """
+    cos_exp = np.repeat(cos, 2, axis=-1)[:, None, :]
+    sin_signed = np.repeat(sin, 2, axis=-1)
+    sin_signed[:, 0::2] *= -1.0
+    sin_signed = sin_signed[:, None, :]
+    swap = np.empty_like(x)
+    swap[..., 0::2] = x[..., 1::2]
+    swap[..., 1::2] = x[..., 0::2]
+    return x * cos_exp + swap * sin_signed
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm
+# ---------------------------------------------------------------------------
+
+def rms_qk(q: torch.Tensor, k: torch.Tensor, gamma_q: torch.Tensor, gamma_k: torch.Tensor,
+           eps: float = EPS):
+    """_tp_rms_qk at TP=1 (models/fast_dit.py:134-147).
+
+    q [B, Lq, C], k [B, Lk, C]; RMS over all C channels of a token; fp32 statistics,
+    `.type_as(x)` rounding, then `* gamma` in the tensors' dtype.
+    """
+    def one(x, g):
+        xf = x.float()
+        inv = torch.rsqrt(xf.pow(2).sum(-1, keepdim=True) / x.shape[-1] + eps)
+        return (xf * inv).type_as(x) * g
+    return one(q, gamma_q), one(k, gamma_k)
+
+
+def rms(x: torch.Tensor, gamma: torch.Tensor, eps: float = EPS) -> torch.Tensor:
+    """_tp_rms at TP=1 (models/fast_dit.py:156-160)."""
+    xf = x.float()
+    ss = xf.pow(2).sum(-1, keepdim=True)
+    return (xf * torch.rsqrt(ss / x.shape[-1] + eps)).type_as(x) * gamma
+
+
+def inv_rms(x: torch.Tensor, eps: float = EPS) -> torch.Tensor:
+    """The per-token statistic 1/sqrt(mean(x^2) + eps), fp32 [B, L]."""
+    xf = x.float()
+    return torch.rsqrt(xf.pow(2).sum(-1) / x.shape[-1] + eps)
+
+
+# ---------------------------------------------------------------------------
+# attention
+# ---------------------------------------------------------------------------
+
+def sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Optional[float] = None,
+         seqlen_k=None) -> torch.Tensor:
+    """softmax(q k^T * scale) v over keys < seqlen_k[b] (models/fast_dit.py:186-189).
+
+    q [B, Lq, n, d], k/v [B, Lk, n, d] -> [B, Lq, n, d], computed by torch's CPU
+    SDPA in the inputs' dtype.  seqlen_k: None (all keys), an int, or one length
+    per sample; keys at or beyond it are excluded (kernels/self_attention_nst.py:73-78).
+    """
+    B, Lk = k.shape[0], k.shape[1]
+    if seqlen_k is None:
+        lens = [Lk] * B
+    elif isinstance(seqlen_k, int):
+        lens = [seqlen_k] * B
+    else:
+        lens = [int(x) for x in seqlen_k]
+    outs = []
+    for b in range(B):
+        n = lens[b]
+        qb = q[b:b + 1].transpose(1, 2)
+        kb = k[b:b + 1, :n].transpose(1, 2)
+        vb = v[b:b + 1, :n].transpose(1, 2)
+        if n == 0:
+            outs.append(torch.zeros_like(q[b:b + 1]))
+            continue
+        ob = F.scaled_dot_product_attention(qb, kb, vb, scale=scale)
+        outs.append(ob.transpose(1, 2))
+    return torch.cat(outs, dim=0)
+
+
+def brute_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: Optional[float] = None,
+                    seqlen_k=None) -> np.ndarray:
+    """float64 per-(batch, head) softmax loop (scripts/validate/attn_bench.py:54-60)."""
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    B, Lq, n, d = q.shape
+    Lk = k.shape[1]
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    lens = [Lk] * B if seqlen_k is None else (
+        [int(seqlen_k)] * B if np.isscalar(seqlen_k) else [int(x) for x in seqlen_k])
+    out = np.zeros((B, Lq, n, d))
+    for b in range(B):
+        m = lens[b]
+        if m == 0:
+            continue
+        for h in range(n):
+            s = q[b, :, h] @ k[b, :m, h].T * scale
+            s = s - s.max(axis=1, keepdims=True)
+            p = np.exp(s)
+            p /= p.sum(axis=1, keepdims=True)
+            out[b, :, h] = p @ v[b, :m, h]
+    return out
+
+
+def self_attn_path(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gamma_q: torch.Tensor,
+                   gamma_k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                   eps: float = EPS, scale: Optional[float] = None) -> torch.Tensor:
+    """QK-RMSNorm -> RoPE -> SDPA, models/fast_dit.py:281-292.  q,k,v [B, L, n, d]."""
+    B, L, n, d = q.shape
+    qn, kn = rms_qk(q.reshape(B, L, n * d), k.reshape(B, L, n * d), gamma_q, gamma_k, eps)
+    qr = rope(qn.view(B, L, n, d), cos, sin)
+    kr = rope(kn.view(B, L, n, d), cos, sin)
+    return sdpa(qr, kr, v, scale=scale)
+
+
+def cross_attn_path(q: torch.Tensor, ck: torch.Tensor, cv: torch.Tensor, gamma_q: torch.Tensor,
+                    eps: float = EPS, seqlen_k=None, scale: Optional[float] = None) -> torch.Tensor:
+    """Cross Q-RMSNorm -> SDPA over the text keys, models/fast_dit.py:297-304."""
+    B, Lq, n, d = q.shape
+    qn = rms(q.reshape(B, Lq, n * d), gamma_q, eps).view(B, Lq, n, d)
+    return sdpa(qn, ck, cv, scale=scale, seqlen_k=seqlen_k)
+
+
+def rel_rms(y: torch.Tensor, ref: torch.Tensor) -> float:
+    """||y - ref||_2 / ||ref||_2 (scripts/validate/attn_bench.py:114-115)."""
+    y = y.double()
+    ref = ref.double()
+    return float((y - ref).pow(2).mean().sqrt() / ref.pow(2).mean().sqrt())

@@ -1,0 +1,260 @@
+"""GPU parity of the HIP attention path against the CPU oracle (oracle/ref.py).
+
+Tolerances (rel-RMS = ||y - y_ref|| / ||y_ref||, scripts/validate/attn_bench.py:114-115):
+  * vs the fp32 CPU SDPA on the same prepared (bf16) q, k, v:  <= 1e-2 (the stated bar);
+    measured values are ~2e-3 and the tests assert <= 5e-3 where noted;
+  * vs the reference's bf16 CPU path (same rounding points):   <= 2^-7 (a couple of bf16 ulps);
+  * vs the float64 golden fixtures (no intermediate rounding): <= 1e-2;
+  * RoPE alone: bit-exact; RMSNorm alone: equal except where the fp32 sum order
+    flips one bf16 rounding (<= 1 ulp, on < 1% of elements).
+Full-size configs (L=7854) are checked on sampled heads against the oracle and on
+all heads through size-independent properties (constant V, masked keys).
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import ref
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+SCALE = D ** -0.5
+DEV = torch.device("cuda:0")
+TOL_FP32 = 1e-2
+TOL_BF16 = 2 ** -7
+
+
+def _bf(shape, seed, std=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * std).to(torch.bfloat16)
+
+
+def _gammas(n, seed, peaky):
+    g = torch.Generator().manual_seed(seed)
+    if not peaky:
+        return torch.ones(n, dtype=torch.bfloat16)
+    # 1 + |N(0,1)| * s: a few channels dominate, as trained QK-norm gammas do
+    return (1 + torch.randn(n, generator=g).abs() * 1.5).to(torch.bfloat16)
+
+
+def _prepared(q, k, gq, gk, grid):
+    """Oracle q, k after QK-RMSNorm and RoPE (bf16, the reference's rounding points)."""
+    B, L, H, _ = q.shape
+    cos, sin = ref.rope_tables(ref.wan_freqs(D), grid, D)
+    qn, kn = ref.rms_qk(q.reshape(B, L, H * D), k.reshape(B, L, H * D), gq, gk)
+    return ref.rope(qn.view(B, L, H, D), cos, sin), ref.rope(kn.view(B, L, H, D), cos, sin), cos, sin
+
+
+def _d(*ts):
+    return [t.to(DEV) for t in ts]
+
+
+# ---------------------------------------------------------------------------
+# golden fixtures (float64, tests/golden/make_golden.py)
+# ---------------------------------------------------------------------------
+
+def test_golden_self_fused(W, golden):
+    q, k, v = (torch.from_numpy(golden[f"self_{n}"]).bfloat16() for n in "qkv")
+    gq, gk = torch.from_numpy(golden["self_gq"]).bfloat16(), torch.from_numpy(golden["self_gk"]).bfloat16()
+    grid = tuple(int(x) for x in golden["self_grid"])
+    cos, sin = ref.rope_tables(ref.wan_freqs(D), grid, D)
+    out = W.ops.self_attn_fused(*_d(q, k, v, gq, gk), 1e-6, *_d(cos, sin), SCALE).cpu()
+    assert ref.rel_rms(out, torch.from_numpy(golden["self_out"])) <= TOL_FP32
+    assert ref.rel_rms(out, ref.self_attn_path(q, k, v, gq, gk, cos, sin)) <= TOL_BF16
+
+
+def test_golden_cross_fused(W, golden):
+    q, ck, cv = (torch.from_numpy(golden[f"cross_{n}"]).bfloat16() for n in "qkv")
+    gq = torch.from_numpy(golden["cross_gq"]).bfloat16()
+    lens = torch.from_numpy(golden["cross_lens"]).int()
+    out = W.ops.cross_attn_fused(*_d(q, ck, cv, gq), 1e-6, lens.to(DEV), SCALE).cpu()
+    assert ref.rel_rms(out, torch.from_numpy(golden["cross_out"])) <= TOL_FP32
+
+
+def test_golden_plain_masked(W, golden):
+    q, k, v = (torch.from_numpy(golden[f"plain_{n}"]).bfloat16() for n in "qkv")
+    out = W.ops.flash_self_attn(*_d(q, k, v), SCALE, int(golden["plain_len"])).cpu()
+    assert ref.rel_rms(out, torch.from_numpy(golden["plain_out"])) <= TOL_FP32
+
+
+# ---------------------------------------------------------------------------
+# plain attention at ragged sizes (tails of the 64-key tile and 128-row block)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("B,Lq,Lk,H,actual", [
+    (1, 1, 1, 1, 0),
+    (1, 5, 3, 2, 0),
+    (1, 64, 64, 1, 0),
+    (2, 63, 65, 3, 0),
+    (1, 129, 200, 2, 129),
+    (2, 257, 77, 2, 0),
+    (1, 300, 300, 2, 1),
+    (1, 1000, 1000, 1, 999),
+])
+def test_plain_self_ragged(W, B, Lq, Lk, H, actual):
+    seed = B * 1000 + Lq + 7 * Lk + H
+    q, k, v = _bf((B, Lq, H, D), seed), _bf((B, Lk, H, D), seed + 1), _bf((B, Lk, H, D), seed + 2)
+    out = W.ops.flash_self_attn(*_d(q, k, v), SCALE, actual).cpu()
+    n = actual if actual > 0 else Lk
+    want32 = ref.sdpa(q.float(), k.float(), v.float(), seqlen_k=n)
+    want16 = ref.sdpa(q, k, v, seqlen_k=n)
+    assert torch.isfinite(out.float()).all()
+    assert ref.rel_rms(out, want32) <= 5e-3
+    assert ref.rel_rms(out, want16) <= TOL_BF16
+
+
+def test_single_key_returns_its_value(W):
+    q, k, v = _bf((2, 77, 3, D), 1), _bf((2, 9, 3, D), 2), _bf((2, 9, 3, D), 3)
+    out = W.ops.flash_self_attn(*_d(q, k, v), SCALE, 1).cpu()
+    assert torch.equal(out, v[:, :1].expand(-1, 77, -1, -1))
+
+
+def test_strided_views(W):
+    """Projections are [B, L, 3072] tensors viewed as [B, L, 24, 128]; also a batch-inner layout."""
+    B, L, H = 2, 150, 24
+    x = _bf((B, L, 3 * H * D), 5)
+    q, k, v = x[..., :H * D].view(B, L, H, D), x[..., H * D:2 * H * D].view(B, L, H, D), x[..., 2 * H * D:].view(B, L, H, D)
+    out = W.ops.flash_self_attn(*_d(q, k, v), SCALE, 0).cpu()
+    assert ref.rel_rms(out, ref.sdpa(q.float(), k.float(), v.float())) <= 5e-3
+    kb = _bf((L, B, H, D), 6).to(DEV).transpose(0, 1)  # batch stride H*D, token stride B*H*D
+    qd, vd = q.contiguous().to(DEV), v.contiguous().to(DEV)
+    out2 = W.ops.flash_self_attn(qd, kb, vd, SCALE, 0).cpu()
+    assert ref.rel_rms(out2, ref.sdpa(q.float(), kb.cpu().float(), v.float())) <= 5e-3
+
+
+# ---------------------------------------------------------------------------
+# fused QK-RMSNorm + RoPE self-attention
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("peaky", [False, True])
+def test_config_a_fused(W, peaky):
+    """B=2, L=1080 (grid 6x12x15), 24 heads: the whole output against the oracle."""
+    B, H, grid = 2, 24, (6, 12, 15)
+    L = grid[0] * grid[1] * grid[2]
+    q, k, v = _bf((B, L, H, D), 11), _bf((B, L, H, D), 12), _bf((B, L, H, D), 13)
+    gq, gk = _gammas(H * D, 14, peaky), _gammas(H * D, 15, peaky)
+    qr, kr, cos, sin = _prepared(q, k, gq, gk, grid)
+    out = W.ops.self_attn_fused(*_d(q, k, v, gq, gk), 1e-6, *_d(cos, sin), SCALE).cpu()
+    assert torch.isfinite(out.float()).all()
+    want32 = ref.sdpa(qr.float(), kr.float(), v.float())
+    e32 = ref.rel_rms(out, want32)
+    e16 = ref.rel_rms(out, ref.sdpa(qr, kr, v))
+    print(f"config A peaky={peaky}: rel_rms vs fp32 {e32:.3e}, vs bf16 path {e16:.3e}")
+    assert e32 <= 5e-3 and e16 <= TOL_BF16
+    # Against the fully fp32 path (norm and rope without bf16 rounding) the kernel is within
+    # the stated bar, or, where the reference's own bf16 rounding of q and k already costs
+    # more than that (peaky gammas: large logits), no further from it than the reference is.
+    full32 = ref.self_attn_path(q.float(), k.float(), v.float(), gq.float(), gk.float(), cos, sin)
+    e_ref = ref.rel_rms(ref.sdpa(qr, kr, v), full32)
+    e_out = ref.rel_rms(out, full32)
+    print(f"config A peaky={peaky}: vs exact fp32 math: kernel {e_out:.3e}, reference bf16 path {e_ref:.3e}")
+    assert e_out <= max(TOL_FP32, 1.1 * e_ref)
+
+
+def test_fused_equals_standalone_ops(W):
+    """fused(q, k, v) == attention(rope(rms(q)), rope(rms(k)), v) from the standalone kernels."""
+    B, H, grid = 2, 6, (3, 5, 7)
+    L = grid[0] * grid[1] * grid[2]
+    q, k, v = _bf((B, L, H, D), 21), _bf((B, L, H, D), 22), _bf((B, L, H, D), 23)
+    gq, gk = _gammas(H * D, 24, True), _gammas(H * D, 25, True)
+    cos, sin = ref.rope_tables(ref.wan_freqs(D), grid, D)
+    qd, kd, vd, gqd, gkd, cd, sd = _d(q, k, v, gq, gk, cos, sin)
+    fused = W.ops.self_attn_fused(qd, kd, vd, gqd, gkd, 1e-6, cd, sd, SCALE)
+    qh = W.ops.rope(W.ops.rms_norm(qd, gqd, 1e-6), cd, sd)
+    kh = W.ops.rope(W.ops.rms_norm(kd, gkd, 1e-6), cd, sd)
+    plain = W.ops.flash_self_attn(qh, kh, vd, SCALE, 0)
+    assert torch.equal(fused, plain)
+
+
+def test_rope_bit_exact(W):
+    B, H, grid = 2, 24, (4, 6, 8)
+    L = grid[0] * grid[1] * grid[2]
+    x = _bf((B, L, H, D), 31, std=3.0)
+    cos, sin = ref.rope_tables(ref.wan_freqs(D), grid, D)
+    out = W.ops.rope(*_d(x, cos, sin)).cpu()
+    assert torch.equal(out, ref.rope(x, cos, sin))
+
+
+def test_rms_norm_matches_reference_rounding(W):
+    B, L, H = 2, 333, 24
+    x = _bf((B, L, H, D), 41, std=2.0)
+    g = _gammas(H * D, 42, True)
+    out = W.ops.rms_norm(*_d(x, g), 1e-6).cpu()
+    want = ref.rms(x.reshape(B, L, H * D), g).view(B, L, H, D)
+    diff = (out.float() - want.float()).abs()
+    ulp = want.float().abs().clamp_min(1e-30) * 2 ** -7
+    assert bool((diff <= ulp).all())
+    assert float((diff > 0).float().mean()) < 1e-2
+    inv = W.ops.rms_inv(x.to(DEV), 1e-6).cpu()
+    assert torch.allclose(inv, ref.inv_rms(x.reshape(B, L, H * D)), rtol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# cross-attention with per-sample key lengths (config B)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("lens", [None, (16, 512), (137, 289), (1, 64), (0, 511)])
+def test_cross_config_b(W, lens):
+    B, H, Lq, Lk = 2, 24, 7854, 512
+    q, ck, cv = _bf((B, Lq, H, D), 51), _bf((B, Lk, H, D), 52), _bf((B, Lk, H, D), 53)
+    gq = _gammas(H * D, 54, True)
+    sk = None if lens is None else torch.tensor(lens, dtype=torch.int32)
+    out = W.ops.cross_attn_fused(*_d(q, ck, cv, gq), 1e-6, None if sk is None else sk.to(DEV), SCALE).cpu()
+    qn = ref.rms(q.reshape(B, Lq, H * D), gq).view(B, Lq, H, D)
+    want = ref.sdpa(qn.float(), ck.float(), cv.float(), seqlen_k=None if lens is None else list(lens))
+    assert torch.isfinite(out.float()).all()
+    if lens is not None and 0 in lens:
+        b0 = lens.index(0)
+        assert torch.count_nonzero(out[b0]) == 0
+        keep = [b for b in range(B) if b != b0]
+        out, want = out[keep], want[keep]
+    assert ref.rel_rms(out, want) <= 5e-3
+
+
+def test_cross_masked_keys_do_not_matter(W):
+    B, H, Lq, Lk = 2, 24, 1000, 512
+    q, ck, cv = _bf((B, Lq, H, D), 61), _bf((B, Lk, H, D), 62), _bf((B, Lk, H, D), 63)
+    lens = torch.tensor([100, 333], dtype=torch.int32)
+    ck2, cv2 = ck.clone(), cv.clone()
+    for b, n in enumerate(lens.tolist()):
+        ck2[b, n:] = _bf((Lk - n, H, D), 64 + b, std=50.0)
+        cv2[b, n:] = float("nan")
+    a = W.ops.cross_attn(*_d(q, ck, cv), lens.to(DEV), SCALE)
+    b = W.ops.cross_attn(*_d(q, ck2, cv2), lens.to(DEV), SCALE)
+    assert torch.equal(a, b)
+
+
+# ---------------------------------------------------------------------------
+# full size self-attention (config C, L=7854 = grid 21x17x22)
+# ---------------------------------------------------------------------------
+
+def test_config_c_fused_sampled_heads(W):
+    B, H, grid = 2, 24, (21, 17, 22)
+    L = grid[0] * grid[1] * grid[2]
+    q, k, v = _bf((B, L, H, D), 71), _bf((B, L, H, D), 72), _bf((B, L, H, D), 73)
+    gq, gk = _gammas(H * D, 74, True), _gammas(H * D, 75, True)
+    qr, kr, cos, sin = _prepared(q, k, gq, gk, grid)
+    out = W.ops.self_attn_fused(*_d(q, k, v, gq, gk), 1e-6, *_d(cos, sin), SCALE).cpu()
+    assert torch.isfinite(out.float()).all()
+    heads = [0, 13, 23]
+    want = ref.sdpa(qr[:, :, heads].float(), kr[:, :, heads].float(), v[:, :, heads].float())
+    e = ref.rel_rms(out[:, :, heads], want)
+    print(f"config C sampled heads {heads}: rel_rms vs fp32 {e:.3e}")
+    assert e <= 5e-3
+
+
+def test_config_c_constant_v(W):
+    """softmax rows sum to one: a per-head constant V comes back unchanged, for every query."""
+    B, H, grid = 2, 24, (21, 17, 22)
+    L = grid[0] * grid[1] * grid[2]
+    q, k = _bf((B, L, H, D), 81), _bf((B, L, H, D), 82)
+    c = _bf((B, 1, H, D), 83)
+    v = c.expand(B, L, H, D).contiguous()
+    gq, gk = _gammas(H * D, 84, True), _gammas(H * D, 85, True)
+    cos, sin = ref.rope_tables(ref.wan_freqs(D), grid, D)
+    out = W.ops.self_attn_fused(*_d(q, k, v, gq, gk), 1e-6, *_d(cos, sin), SCALE).cpu().float()
+    want = c.float().expand(B, L, H, D)
+    rel = ((out - want).abs() / want.abs().clamp_min(1e-3)).max()
+    assert float(rel) <= 2 ** -7

@@ -1,0 +1,113 @@
+"""The C ABI library on the CPU: it loads, exports every function include/wan_attn.h
+declares, and rejects bad arguments before any device work.  No kernel is launched.
+"""
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "wan_attn.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(wan_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points():
+    names = header_functions()
+    for n in ("wan_flash_self_attn", "wan_cross_attn", "wan_self_attn_fused", "wan_cross_attn_fused",
+              "wan_rope", "wan_rms_norm", "wan_attn_last_error"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(W):
+    lib = W._native.lib()
+    missing = [n for n in header_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(W._native.SIGNATURES) == set(header_functions())
+
+
+def test_abi_version(W):
+    assert W._native.lib().wan_attn_abi_version() == W._native.ABI_VERSION
+
+
+def test_validation_rejects_bad_arguments_without_launching(W):
+    N = W._native
+    lib = N.lib()
+    ok = N.WanTensor(64, 24 * 128 * 16, 24 * 128, 128)
+    # head_dim other than 128 is unsupported
+    rc = lib.wan_flash_self_attn(ok, ok, ok, ok, 1, 24, 16, 16, 64, 0.1, 0, None)
+    assert rc == 2 and "head_dim" in N.last_error()
+    # misaligned pointer
+    bad = N.WanTensor(66, 24 * 128 * 16, 24 * 128, 128)
+    rc = lib.wan_flash_self_attn(bad, ok, ok, ok, 1, 24, 16, 16, 128, 0.1, 0, None)
+    assert rc == 1 and "aligned" in N.last_error()
+    # stride not a multiple of 8
+    bad = N.WanTensor(64, 24 * 128 * 16, 24 * 128 + 4, 128)
+    rc = lib.wan_flash_self_attn(ok, bad, ok, ok, 1, 24, 16, 16, 128, 0.1, 0, None)
+    assert rc == 1 and "stride" in N.last_error()
+    # actual_seqlen_k beyond the keys
+    rc = lib.wan_flash_self_attn(ok, ok, ok, ok, 1, 24, 16, 16, 128, 0.1, 17, None)
+    assert rc == 1 and "actual_seqlen_k" in N.last_error()
+    # NULL operand
+    rc = lib.wan_cross_attn(ok, N.WanTensor(0, 0, 0, 0), ok, ok, 1, 24, 16, 16, 128, 0.1, None, None)
+    assert rc == 1 and "NULL" in N.last_error()
+    # fused: workspace too small / missing tables
+    rc = lib.wan_self_attn_fused(ok, ok, ok, ok, 1, 24, 16, 128, 256, 256, 1e-6, 256, 256, 0.1,
+                                 256, 10, None)
+    assert rc == 3 and "workspace" in N.last_error()
+    rc = lib.wan_self_attn_fused(ok, ok, ok, ok, 1, 24, 16, 128, None, 256, 1e-6, 256, 256, 0.1,
+                                 256, 1 << 30, None)
+    assert rc == 1
+    rc = lib.wan_cross_attn_fused(ok, ok, ok, ok, 1, 24, 16, 8, 128, 256, -1.0, 0.1, None, 256,
+                                  1 << 30, None)
+    assert rc == 1 and "eps" in N.last_error()
+    # rms_norm: rotation without an output, one table missing
+    rc = lib.wan_rms_norm(ok, None, 1, 16, 24, 128, 256, 1e-6, 256, 256, None, None)
+    assert rc == 1 and "out" in N.last_error()
+    rc = lib.wan_rms_norm(ok, 256, 1, 16, 24, 128, 256, 1e-6, 256, None, None, None)
+    assert rc == 1 and "both" in N.last_error()
+    rc = lib.wan_flash_attn_qnorm(ok, ok, ok, ok, 1, 24, 16, 16, 128, None, 256, None, None, 0.1,
+                                  None, None)
+    assert rc == 1 and "inv_rms_q" in N.last_error()
+    # nothing to do is not an error
+    assert lib.wan_flash_self_attn(ok, ok, ok, ok, 0, 24, 16, 16, 128, 0.1, 0, None) == 0
+
+
+def test_workspace_sizes(W):
+    lib = W._native.lib()
+    B, H, L = 2, 24, 7854
+    ws = lib.wan_self_attn_fused_workspace(B, H, L)
+    assert ws >= B * L * 4 + B * L * H * 128 * 2 and ws % 256 == 0
+    assert lib.wan_cross_attn_fused_workspace(B, H, L) >= B * L * 4
+    assert lib.wan_self_attn_fused_workspace(0, H, L) == 0
+
+
+def test_ops_fail_loudly_on_host_tensors(W):
+    q = torch.zeros(1, 8, 2, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="CUDA"):
+        W.ops.flash_self_attn(q, q, q, 0.1, 0)
+    with pytest.raises(ValueError, match="CUDA"):
+        W.ops.cross_attn(q, q, q, None, 0.1)
+
+
+def test_ops_validate_layout(W):
+    q = torch.zeros(1, 8, 2, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="head_dim"):
+        W.ops.flash_self_attn(q, q, q, 0.1, 0)
+    q = torch.zeros(1, 8, 2, 128, dtype=torch.float32)
+    with pytest.raises(ValueError, match="bfloat16"):
+        W.ops.flash_self_attn(q, q, q, 0.1, 0)
+
+
+def test_custom_ops_have_fake_kernels(W):
+    """torch.compile can trace the ops without running them (meta tensors)."""
+    q = torch.empty(2, 100, 4, 128, dtype=torch.bfloat16, device="meta")
+    out = torch.ops.wan_hip.flash_self_attn(q, q, q, 0.1, 0)
+    assert out.shape == q.shape and out.device.type == "meta"
+    out = torch.ops.wan_hip.cross_attn(q, q[:, :7], q[:, :7], None, 0.1)
+    assert out.shape == q.shape

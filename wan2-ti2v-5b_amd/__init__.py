@@ -1,0 +1,17 @@
+"""MI355X (gfx950) attention hot path of the Wan2.2-TI2V-5B DiT.
+
+Layout of the package:
+  csrc/          HIP kernels (flash attention, QK-RMSNorm / RoPE prep) and the C ABI
+                 declared in include/wan_attn.h, built into libwan_attn.so by build.py
+  _native.py     ctypes binding of that C ABI
+  ops.py         torch.library custom ops over it (wan_hip::*)
+  rope.py        3D-RoPE angle tables (host side, once per grid)
+  attention.py   attention() dispatch of wan/modules/attention.py
+  fast_dit.py    the FAST_ATTN_IMPL-selected backends and block span of models/fast_dit.py
+
+The directory name is not a Python identifier; load it as the module
+`wan2_ti2v_5b_amd` (see load_package() in __graft_entry__.py).
+"""
+from . import _native, ops, rope  # noqa: F401
+
+__all__ = ["_native", "ops", "rope"]

@@ -1,0 +1,306 @@
+// C-ABI entry points (include/wan_attn.h): argument validation, workspace
+// layout and dispatch to the kernels.  Nothing here allocates device memory
+// or synchronises the stream.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/wan_attn.h"
+#include "common.h"
+
+namespace wan {
+
+namespace {
+thread_local char g_last_error[512] = "";
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t n) { return (n + kAlign - 1) / kAlign * kAlign; }
+
+Tensor4 as_t4(const wan_tensor& t) {
+  return Tensor4{static_cast<const bf16*>(t.data), t.batch_stride, t.token_stride, t.head_stride};
+}
+
+// Checks one [B, L, H, 128] operand: pointer, alignment, stride granularity.
+int check_tensor(const char* fn, const char* name, const wan_tensor& t, int B, int L, int H) {
+  if (B > 0 && L > 0 && H > 0 && t.data == nullptr)
+    return set_error(WAN_ERR_INVALID, "%s: %s is NULL", fn, name);
+  if (reinterpret_cast<uintptr_t>(t.data) % 16 != 0)
+    return set_error(WAN_ERR_INVALID, "%s: %s is not 16-byte aligned", fn, name);
+  if (t.batch_stride % 8 || t.token_stride % 8 || t.head_stride % 8)
+    return set_error(WAN_ERR_INVALID,
+                     "%s: %s strides (%lld, %lld, %lld) must be multiples of 8 elements", fn, name,
+                     (long long)t.batch_stride, (long long)t.token_stride, (long long)t.head_stride);
+  if (t.batch_stride < 0 || t.token_stride < 0 || t.head_stride < 0)
+    return set_error(WAN_ERR_INVALID, "%s: %s has a negative stride", fn, name);
+  return WAN_OK;
+}
+
+int check_dims(const char* fn, int B, int H, int Lq, int Lk, int D) {
+  if (B < 0 || H < 0 || Lq < 0 || Lk < 0)
+    return set_error(WAN_ERR_INVALID, "%s: negative size (B=%d H=%d Lq=%d Lk=%d)", fn, B, H, Lq, Lk);
+  if (D != kHeadDim)
+    return set_error(WAN_ERR_UNSUPPORTED, "%s: head_dim=%d, only 128 is implemented", fn, D);
+  if (H * kHeadDim > 8192)
+    return set_error(WAN_ERR_UNSUPPORTED, "%s: heads*128=%d exceeds 8192 channels", fn, H * kHeadDim);
+  return WAN_OK;
+}
+
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+}  // namespace
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+}  // namespace wan
+
+using namespace wan;
+
+extern "C" {
+
+const char* wan_attn_last_error(void) { return g_last_error; }
+
+int wan_attn_abi_version(void) { return 1; }
+
+int wan_flash_self_attn(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor out, int batch,
+                        int heads, int seqlen_q, int seqlen_k, int head_dim, float softmax_scale,
+                        int actual_seqlen_k, void* stream) {
+  const char* fn = "wan_flash_self_attn";
+  int rc;
+  if ((rc = check_dims(fn, batch, heads, seqlen_q, seqlen_k, head_dim))) return rc;
+  if ((rc = check_tensor(fn, "q", q, batch, seqlen_q, heads))) return rc;
+  if ((rc = check_tensor(fn, "k", k, batch, seqlen_k, heads))) return rc;
+  if ((rc = check_tensor(fn, "v", v, batch, seqlen_k, heads))) return rc;
+  if ((rc = check_tensor(fn, "out", out, batch, seqlen_q, heads))) return rc;
+  if (actual_seqlen_k <= 0) actual_seqlen_k = seqlen_k;
+  if (actual_seqlen_k > seqlen_k)
+    return set_error(WAN_ERR_INVALID, "%s: actual_seqlen_k=%d exceeds seqlen_k=%d", fn,
+                     actual_seqlen_k, seqlen_k);
+  if (seqlen_q > 0 && seqlen_k == 0)
+    return set_error(WAN_ERR_INVALID, "%s: no keys (seqlen_k=0)", fn);
+  FlashArgs a{};
+  a.q = as_t4(q);
+  a.k = as_t4(k);
+  a.v = as_t4(v);
+  a.o = static_cast<bf16*>(out.data);
+  a.o_sb = out.batch_stride;
+  a.o_st = out.token_stride;
+  a.o_sh = out.head_stride;
+  a.B = batch;
+  a.H = heads;
+  a.Lq = seqlen_q;
+  a.Lk = seqlen_k;
+  a.seqlen_k = nullptr;
+  a.seqlen_all = actual_seqlen_k;
+  a.scale = softmax_scale;
+  a.qprep = kQPlain;
+  return launch_flash_fwd(a, static_cast<hipStream_t>(stream));
+}
+
+int wan_cross_attn(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor out, int batch, int heads,
+                   int seqlen_q, int seqlen_k, int head_dim, float softmax_scale,
+                   const int32_t* seqlen_k_dev, void* stream) {
+  const char* fn = "wan_cross_attn";
+  int rc;
+  if ((rc = check_dims(fn, batch, heads, seqlen_q, seqlen_k, head_dim))) return rc;
+  if ((rc = check_tensor(fn, "q", q, batch, seqlen_q, heads))) return rc;
+  if ((rc = check_tensor(fn, "k", k, batch, seqlen_k, heads))) return rc;
+  if ((rc = check_tensor(fn, "v", v, batch, seqlen_k, heads))) return rc;
+  if ((rc = check_tensor(fn, "out", out, batch, seqlen_q, heads))) return rc;
+  FlashArgs a{};
+  a.q = as_t4(q);
+  a.k = as_t4(k);
+  a.v = as_t4(v);
+  a.o = static_cast<bf16*>(out.data);
+  a.o_sb = out.batch_stride;
+  a.o_st = out.token_stride;
+  a.o_sh = out.head_stride;
+  a.B = batch;
+  a.H = heads;
+  a.Lq = seqlen_q;
+  a.Lk = seqlen_k;
+  a.seqlen_k = seqlen_k_dev;
+  a.seqlen_all = seqlen_k;
+  a.scale = softmax_scale;
+  a.qprep = kQPlain;
+  return launch_flash_fwd(a, static_cast<hipStream_t>(stream));
+}
+
+size_t wan_self_attn_fused_workspace(int batch, int heads, int seqlen) {
+  if (batch <= 0 || heads <= 0 || seqlen <= 0) return 0;
+  const size_t rows = (size_t)batch * seqlen;
+  return align_up(rows * sizeof(float)) + align_up(rows * heads * kHeadDim * sizeof(bf16));
+}
+
+int wan_rms_norm(wan_tensor x, void* out, int batch, int seqlen, int heads, int head_dim,
+                 const void* gamma, float eps, const float* rope_cos, const float* rope_sin,
+                 float* inv_rms_out, void* stream) {
+  const char* fn = "wan_rms_norm";
+  int rc;
+  if ((rc = check_dims(fn, batch, heads, seqlen, seqlen, head_dim))) return rc;
+  if ((rc = check_tensor(fn, "x", x, batch, seqlen, heads))) return rc;
+  if ((int64_t)batch * seqlen * heads == 0) return WAN_OK;
+  if (out && !aligned16(out)) return set_error(WAN_ERR_INVALID, "%s: out must be 16-byte aligned", fn);
+  if (out && (!gamma || !aligned16(gamma)))
+    return set_error(WAN_ERR_INVALID, "%s: gamma must be a 16-byte aligned pointer", fn);
+  if ((rope_cos == nullptr) != (rope_sin == nullptr))
+    return set_error(WAN_ERR_INVALID, "%s: rope_cos and rope_sin must both be given or both NULL", fn);
+  if (rope_cos && (!out || !aligned16(rope_cos) || !aligned16(rope_sin)))
+    return set_error(WAN_ERR_INVALID, "%s: rotation needs `out` and 16-byte aligned tables", fn);
+  if (!(eps >= 0.f)) return set_error(WAN_ERR_INVALID, "%s: eps must be >= 0", fn);
+  PrepArgs a{};
+  a.x = as_t4(x);
+  a.B = batch;
+  a.L = seqlen;
+  a.H = heads;
+  a.eps = eps;
+  a.inv_rms = inv_rms_out;
+  a.gamma = static_cast<const bf16*>(gamma);
+  a.cos = rope_cos;
+  a.sin = rope_sin;
+  a.out = static_cast<bf16*>(out);
+  return launch_rms_prep(a, static_cast<hipStream_t>(stream));
+}
+
+int wan_flash_attn_qnorm(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor out, int batch,
+                         int heads, int seqlen_q, int seqlen_k, int head_dim,
+                         const float* inv_rms_q, const void* gamma_q, const float* rope_cos,
+                         const float* rope_sin, float softmax_scale, const int32_t* seqlen_k_dev,
+                         void* stream) {
+  const char* fn = "wan_flash_attn_qnorm";
+  int rc;
+  if ((rc = check_dims(fn, batch, heads, seqlen_q, seqlen_k, head_dim))) return rc;
+  if ((rc = check_tensor(fn, "q", q, batch, seqlen_q, heads))) return rc;
+  if ((rc = check_tensor(fn, "k", k, batch, seqlen_k, heads))) return rc;
+  if ((rc = check_tensor(fn, "v", v, batch, seqlen_k, heads))) return rc;
+  if ((rc = check_tensor(fn, "out", out, batch, seqlen_q, heads))) return rc;
+  if (batch == 0 || heads == 0 || seqlen_q == 0) return WAN_OK;
+  if (!inv_rms_q || !gamma_q || !aligned16(gamma_q))
+    return set_error(WAN_ERR_INVALID, "%s: inv_rms_q and a 16-byte aligned gamma_q are required", fn);
+  if ((rope_cos == nullptr) != (rope_sin == nullptr))
+    return set_error(WAN_ERR_INVALID, "%s: rope_cos and rope_sin must both be given or both NULL", fn);
+  if (rope_cos && (!aligned16(rope_cos) || !aligned16(rope_sin)))
+    return set_error(WAN_ERR_INVALID, "%s: rope tables must be 16-byte aligned", fn);
+  FlashArgs a{};
+  a.q = as_t4(q);
+  a.k = as_t4(k);
+  a.v = as_t4(v);
+  a.o = static_cast<bf16*>(out.data);
+  a.o_sb = out.batch_stride;
+  a.o_st = out.token_stride;
+  a.o_sh = out.head_stride;
+  a.B = batch;
+  a.H = heads;
+  a.Lq = seqlen_q;
+  a.Lk = seqlen_k;
+  a.seqlen_k = seqlen_k_dev;
+  a.seqlen_all = seqlen_k;
+  a.scale = softmax_scale;
+  a.qprep = rope_cos ? kQNormRope : kQNorm;
+  a.inv_rms_q = inv_rms_q;
+  a.gamma_q = static_cast<const bf16*>(gamma_q);
+  a.cos = rope_cos;
+  a.sin = rope_sin;
+  return launch_flash_fwd(a, static_cast<hipStream_t>(stream));
+}
+
+int wan_self_attn_fused(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor out, int batch,
+                        int heads, int seqlen, int head_dim, const void* gamma_q,
+                        const void* gamma_k, float eps, const float* rope_cos,
+                        const float* rope_sin, float softmax_scale, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  const char* fn = "wan_self_attn_fused";
+  int rc;
+  if ((rc = check_dims(fn, batch, heads, seqlen, seqlen, head_dim))) return rc;
+  if ((rc = check_tensor(fn, "q", q, batch, seqlen, heads))) return rc;
+  if ((rc = check_tensor(fn, "k", k, batch, seqlen, heads))) return rc;
+  if ((rc = check_tensor(fn, "v", v, batch, seqlen, heads))) return rc;
+  if ((rc = check_tensor(fn, "out", out, batch, seqlen, heads))) return rc;
+  if (batch == 0 || heads == 0 || seqlen == 0) return WAN_OK;
+  if (!gamma_q || !gamma_k || !rope_cos || !rope_sin)
+    return set_error(WAN_ERR_INVALID, "%s: gamma_q, gamma_k, rope_cos and rope_sin are required", fn);
+  if (!aligned16(gamma_q) || !aligned16(gamma_k) || !aligned16(rope_cos) || !aligned16(rope_sin))
+    return set_error(WAN_ERR_INVALID, "%s: gamma and rope tables must be 16-byte aligned", fn);
+  if (!(eps >= 0.f)) return set_error(WAN_ERR_INVALID, "%s: eps must be >= 0", fn);
+  const size_t need = wan_self_attn_fused_workspace(batch, heads, seqlen);
+  if (workspace == nullptr || workspace_bytes < need)
+    return set_error(WAN_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, %zu given", fn, need,
+                     workspace ? workspace_bytes : (size_t)0);
+  if (reinterpret_cast<uintptr_t>(workspace) % kAlign)
+    return set_error(WAN_ERR_INVALID, "%s: workspace must be 256-byte aligned", fn);
+  const size_t rows = (size_t)batch * seqlen;
+  float* inv_q = static_cast<float*>(workspace);
+  void* khat = static_cast<char*>(workspace) + align_up(rows * sizeof(float));
+  const wan_tensor kt{khat, (int64_t)seqlen * heads * kHeadDim, (int64_t)heads * kHeadDim, kHeadDim};
+  if ((rc = wan_rms_norm(q, nullptr, batch, seqlen, heads, head_dim, nullptr, eps, nullptr,
+                         nullptr, inv_q, stream)))
+    return rc;
+  if ((rc = wan_rms_norm(k, khat, batch, seqlen, heads, head_dim, gamma_k, eps, rope_cos, rope_sin,
+                         nullptr, stream)))
+    return rc;
+  return wan_flash_attn_qnorm(q, kt, v, out, batch, heads, seqlen, seqlen, head_dim, inv_q, gamma_q,
+                              rope_cos, rope_sin, softmax_scale, nullptr, stream);
+}
+
+size_t wan_cross_attn_fused_workspace(int batch, int heads, int seqlen_q) {
+  (void)heads;
+  if (batch <= 0 || seqlen_q <= 0) return 0;
+  return align_up((size_t)batch * seqlen_q * sizeof(float));
+}
+
+int wan_cross_attn_fused(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor out, int batch,
+                         int heads, int seqlen_q, int seqlen_k, int head_dim, const void* gamma_q,
+                         float eps, float softmax_scale, const int32_t* seqlen_k_dev,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "wan_cross_attn_fused";
+  int rc;
+  if ((rc = check_dims(fn, batch, heads, seqlen_q, seqlen_k, head_dim))) return rc;
+  if ((rc = check_tensor(fn, "q", q, batch, seqlen_q, heads))) return rc;
+  if ((rc = check_tensor(fn, "k", k, batch, seqlen_k, heads))) return rc;
+  if ((rc = check_tensor(fn, "v", v, batch, seqlen_k, heads))) return rc;
+  if ((rc = check_tensor(fn, "out", out, batch, seqlen_q, heads))) return rc;
+  if (batch == 0 || heads == 0 || seqlen_q == 0) return WAN_OK;
+  if (!gamma_q || !aligned16(gamma_q))
+    return set_error(WAN_ERR_INVALID, "%s: gamma_q must be a 16-byte aligned pointer", fn);
+  if (!(eps >= 0.f)) return set_error(WAN_ERR_INVALID, "%s: eps must be >= 0", fn);
+  const size_t need = wan_cross_attn_fused_workspace(batch, heads, seqlen_q);
+  if (workspace == nullptr || workspace_bytes < need)
+    return set_error(WAN_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, %zu given", fn, need,
+                     workspace ? workspace_bytes : (size_t)0);
+  if (reinterpret_cast<uintptr_t>(workspace) % kAlign)
+    return set_error(WAN_ERR_INVALID, "%s: workspace must be 256-byte aligned", fn);
+  float* inv_q = static_cast<float*>(workspace);
+  if ((rc = wan_rms_norm(q, nullptr, batch, seqlen_q, heads, head_dim, nullptr, eps, nullptr,
+                         nullptr, inv_q, stream)))
+    return rc;
+  return wan_flash_attn_qnorm(q, k, v, out, batch, heads, seqlen_q, seqlen_k, head_dim, inv_q,
+                              gamma_q, nullptr, nullptr, softmax_scale, seqlen_k_dev, stream);
+}
+
+int wan_rope(wan_tensor x, void* out, int batch, int seqlen, int heads, int head_dim,
+             const float* rope_cos, const float* rope_sin, void* stream) {
+  const char* fn = "wan_rope";
+  int rc;
+  if ((rc = check_dims(fn, batch, heads, seqlen, seqlen, head_dim))) return rc;
+  if ((rc = check_tensor(fn, "x", x, batch, seqlen, heads))) return rc;
+  if ((int64_t)batch * seqlen * heads == 0) return WAN_OK;
+  if (!out || !aligned16(out)) return set_error(WAN_ERR_INVALID, "%s: out must be a 16-byte aligned pointer", fn);
+  if (!rope_cos || !rope_sin || !aligned16(rope_cos) || !aligned16(rope_sin))
+    return set_error(WAN_ERR_INVALID, "%s: rope tables must be 16-byte aligned pointers", fn);
+  RopeArgs a{};
+  a.x = as_t4(x);
+  a.B = batch;
+  a.L = seqlen;
+  a.H = heads;
+  a.cos = rope_cos;
+  a.sin = rope_sin;
+  a.out = static_cast<bf16*>(out);
+  return launch_rope(a, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

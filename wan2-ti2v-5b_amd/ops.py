@@ -1,0 +1,281 @@
+"""torch operators over the C ABI (torch.library custom ops with fake kernels).
+
+Every op takes bf16 CUDA tensors in the DiT projection layout [B, L, H, 128]
+(views of [B, L, 3072] are accepted as they are: only the head_dim axis must be
+contiguous), launches on torch's current stream of the tensor's device and
+returns a new contiguous [B, Lq, H, 128] tensor.  Outputs and workspaces come
+from torch's caching allocator; the native side allocates nothing.
+
+The fake (meta) kernels let torch.compile trace the ops without running them.
+"""
+from typing import Optional
+
+import torch
+
+from . import _native as N
+
+HEAD_DIM = 128
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _check4(name: str, x: torch.Tensor) -> None:
+    if not isinstance(x, torch.Tensor):
+        raise TypeError(f"{name}: expected a tensor, got {type(x).__name__}")
+    if x.dim() != 4:
+        raise ValueError(f"{name}: expected [B, L, H, {HEAD_DIM}], got shape {tuple(x.shape)}")
+    if x.shape[-1] != HEAD_DIM:
+        raise ValueError(f"{name}: head_dim must be {HEAD_DIM}, got {x.shape[-1]}")
+    if x.dtype != torch.bfloat16:
+        raise ValueError(f"{name}: expected bfloat16, got {x.dtype}")
+    if x.device.type != "cuda":
+        raise ValueError(f"{name}: expected a CUDA (HIP) tensor, got device {x.device}")
+    if x.numel() == 0:
+        return
+    if x.stride(-1) != 1:
+        raise ValueError(f"{name}: the head_dim axis must be contiguous (stride {x.stride(-1)})")
+    if any(s % 8 for s in x.stride()[:3]) or x.data_ptr() % 16:
+        raise ValueError(f"{name}: strides {x.stride()} must be multiples of 8 elements "
+                         "and the data 16-byte aligned")
+
+
+def _check_qkv(fn: str, q, k, v):
+    _check4(f"{fn}: q", q)
+    _check4(f"{fn}: k", k)
+    _check4(f"{fn}: v", v)
+    if k.shape != v.shape:
+        raise ValueError(f"{fn}: k {tuple(k.shape)} and v {tuple(v.shape)} differ")
+    if q.shape[0] != k.shape[0] or q.shape[2] != k.shape[2]:
+        raise ValueError(f"{fn}: q {tuple(q.shape)} and k {tuple(k.shape)} disagree on batch/heads")
+    if not (q.device == k.device == v.device):
+        raise ValueError(f"{fn}: q, k, v are on different devices")
+
+
+def _check_vec(fn: str, name: str, t: torch.Tensor, n: int, dtype, device) -> None:
+    if t.device != device or t.dtype != dtype or t.numel() != n or not t.is_contiguous():
+        raise ValueError(f"{fn}: {name} must be a contiguous {dtype} tensor of {n} elements on "
+                         f"{device}, got {t.dtype} {tuple(t.shape)} on {t.device}")
+
+
+def _check_rope(fn: str, cos: torch.Tensor, sin: torch.Tensor, L: int, device) -> None:
+    for name, t in (("cos", cos), ("sin", sin)):
+        if t.device != device or t.dtype != torch.float32 or not t.is_contiguous() \
+                or t.numel() != L * HEAD_DIM // 2:
+            raise ValueError(f"{fn}: {name} must be a contiguous float32 [{L}, {HEAD_DIM // 2}] "
+                             f"tensor on {device}, got {t.dtype} {tuple(t.shape)} on {t.device}")
+
+
+def _seqlen_ptr(fn: str, seqlen_k: Optional[torch.Tensor], B: int, device) -> int:
+    if seqlen_k is None:
+        return 0
+    _check_vec(fn, "seqlen_k", seqlen_k, B, torch.int32, device)
+    return seqlen_k.data_ptr()
+
+
+# ---------------------------------------------------------------------------
+# self-attention (kernels/self_attention_nst.py:49-117; models/fast_dit.py:186-207)
+# ---------------------------------------------------------------------------
+
+@torch.library.custom_op("wan_hip::flash_self_attn", mutates_args=())
+def flash_self_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                    softmax_scale: float, actual_seqlen_k: int) -> torch.Tensor:
+    fn = "flash_self_attn"
+    _check_qkv(fn, q, k, v)
+    B, Lq, H, D = q.shape
+    Lk = k.shape[1]
+    if actual_seqlen_k > Lk:
+        raise ValueError(f"{fn}: actual_seqlen_k must be in (0, {Lk}], got {actual_seqlen_k}")
+    out = torch.empty((B, Lq, H, D), dtype=q.dtype, device=q.device)
+    with torch.cuda.device(q.device):
+        N.check("wan_flash_self_attn", N.lib().wan_flash_self_attn(
+            N.tensor4(q), N.tensor4(k), N.tensor4(v), N.tensor4(out), B, H, Lq, Lk, D,
+            float(softmax_scale), int(actual_seqlen_k), _stream(q.device)))
+    return out
+
+
+@flash_self_attn.register_fake
+def _(q, k, v, softmax_scale, actual_seqlen_k):
+    return q.new_empty(q.shape)
+
+
+@torch.library.custom_op("wan_hip::cross_attn", mutates_args=())
+def cross_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+               seqlen_k: Optional[torch.Tensor], softmax_scale: float) -> torch.Tensor:
+    fn = "cross_attn"
+    _check_qkv(fn, q, k, v)
+    B, Lq, H, D = q.shape
+    Lk = k.shape[1]
+    sk = _seqlen_ptr(fn, seqlen_k, B, q.device)
+    out = torch.empty((B, Lq, H, D), dtype=q.dtype, device=q.device)
+    with torch.cuda.device(q.device):
+        N.check("wan_cross_attn", N.lib().wan_cross_attn(
+            N.tensor4(q), N.tensor4(k), N.tensor4(v), N.tensor4(out), B, H, Lq, Lk, D,
+            float(softmax_scale), sk, _stream(q.device)))
+    return out
+
+
+@cross_attn.register_fake
+def _(q, k, v, seqlen_k, softmax_scale):
+    return q.new_empty(q.shape)
+
+
+# ---------------------------------------------------------------------------
+# fused spans of _FastBlock.forward (models/fast_dit.py:281-292 and :297-304)
+# ---------------------------------------------------------------------------
+
+@torch.library.custom_op("wan_hip::self_attn_fused", mutates_args=())
+def self_attn_fused(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                    gamma_q: torch.Tensor, gamma_k: torch.Tensor, eps: float,
+                    cos: torch.Tensor, sin: torch.Tensor, softmax_scale: float) -> torch.Tensor:
+    fn = "self_attn_fused"
+    _check_qkv(fn, q, k, v)
+    B, L, H, D = q.shape
+    if k.shape[1] != L:
+        raise ValueError(f"{fn}: self-attention needs Lq == Lk, got {L} and {k.shape[1]}")
+    _check_vec(fn, "gamma_q", gamma_q, H * D, torch.bfloat16, q.device)
+    _check_vec(fn, "gamma_k", gamma_k, H * D, torch.bfloat16, q.device)
+    _check_rope(fn, cos, sin, L, q.device)
+    lib = N.lib()
+    ws = torch.empty(max(1, lib.wan_self_attn_fused_workspace(B, H, L)), dtype=torch.uint8,
+                     device=q.device)
+    out = torch.empty((B, L, H, D), dtype=q.dtype, device=q.device)
+    with torch.cuda.device(q.device):
+        N.check("wan_self_attn_fused", lib.wan_self_attn_fused(
+            N.tensor4(q), N.tensor4(k), N.tensor4(v), N.tensor4(out), B, H, L, D,
+            gamma_q.data_ptr(), gamma_k.data_ptr(), float(eps), cos.data_ptr(), sin.data_ptr(),
+            float(softmax_scale), ws.data_ptr(), ws.numel(), _stream(q.device)))
+    return out
+
+
+@self_attn_fused.register_fake
+def _(q, k, v, gamma_q, gamma_k, eps, cos, sin, softmax_scale):
+    return q.new_empty(q.shape)
+
+
+@torch.library.custom_op("wan_hip::cross_attn_fused", mutates_args=())
+def cross_attn_fused(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gamma_q: torch.Tensor,
+                     eps: float, seqlen_k: Optional[torch.Tensor],
+                     softmax_scale: float) -> torch.Tensor:
+    fn = "cross_attn_fused"
+    _check_qkv(fn, q, k, v)
+    B, Lq, H, D = q.shape
+    Lk = k.shape[1]
+    _check_vec(fn, "gamma_q", gamma_q, H * D, torch.bfloat16, q.device)
+    sk = _seqlen_ptr(fn, seqlen_k, B, q.device)
+    lib = N.lib()
+    ws = torch.empty(max(1, lib.wan_cross_attn_fused_workspace(B, H, Lq)), dtype=torch.uint8,
+                     device=q.device)
+    out = torch.empty((B, Lq, H, D), dtype=q.dtype, device=q.device)
+    with torch.cuda.device(q.device):
+        N.check("wan_cross_attn_fused", lib.wan_cross_attn_fused(
+            N.tensor4(q), N.tensor4(k), N.tensor4(v), N.tensor4(out), B, H, Lq, Lk, D,
+            gamma_q.data_ptr(), float(eps), float(softmax_scale), sk, ws.data_ptr(), ws.numel(),
+            _stream(q.device)))
+    return out
+
+
+@cross_attn_fused.register_fake
+def _(q, k, v, gamma_q, eps, seqlen_k, softmax_scale):
+    return q.new_empty(q.shape)
+
+
+# ---------------------------------------------------------------------------
+# standalone RoPE and RMSNorm (models/fast_dit.py:163-169, :156-160; kernels/rope.py:39-71)
+# ---------------------------------------------------------------------------
+
+@torch.library.custom_op("wan_hip::rope", mutates_args=())
+def rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    fn = "rope"
+    _check4(f"{fn}: x", x)
+    B, L, H, D = x.shape
+    _check_rope(fn, cos, sin, L, x.device)
+    out = torch.empty((B, L, H, D), dtype=x.dtype, device=x.device)
+    with torch.cuda.device(x.device):
+        N.check("wan_rope", N.lib().wan_rope(N.tensor4(x), out.data_ptr(), B, L, H, D,
+                                             cos.data_ptr(), sin.data_ptr(), _stream(x.device)))
+    return out
+
+
+@rope.register_fake
+def _(x, cos, sin):
+    return x.new_empty(x.shape)
+
+
+def _rms_call(x, gamma, eps, cos, sin, out, inv):
+    B, L, H, D = x.shape
+    with torch.cuda.device(x.device):
+        N.check("wan_rms_norm", N.lib().wan_rms_norm(
+            N.tensor4(x), None if out is None else out.data_ptr(), B, L, H, D,
+            None if gamma is None else gamma.data_ptr(), float(eps),
+            None if cos is None else cos.data_ptr(), None if sin is None else sin.data_ptr(),
+            None if inv is None else inv.data_ptr(), _stream(x.device)))
+
+
+@torch.library.custom_op("wan_hip::rms_norm", mutates_args=())
+def rms_norm(x: torch.Tensor, gamma: torch.Tensor, eps: float,
+             cos: Optional[torch.Tensor] = None, sin: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """_tp_rms over all H*128 channels of each token (optionally followed by _rope)."""
+    fn = "rms_norm"
+    _check4(f"{fn}: x", x)
+    B, L, H, D = x.shape
+    _check_vec(fn, "gamma", gamma, H * D, torch.bfloat16, x.device)
+    if (cos is None) != (sin is None):
+        raise ValueError(f"{fn}: give both cos and sin, or neither")
+    if cos is not None:
+        _check_rope(fn, cos, sin, L, x.device)
+    out = torch.empty((B, L, H, D), dtype=x.dtype, device=x.device)
+    _rms_call(x, gamma, eps, cos, sin, out, None)
+    return out
+
+
+@rms_norm.register_fake
+def _(x, gamma, eps, cos=None, sin=None):
+    return x.new_empty(x.shape)
+
+
+@torch.library.custom_op("wan_hip::rms_inv", mutates_args=())
+def rms_inv(x: torch.Tensor, eps: float) -> torch.Tensor:
+    """Per-token 1/rms over all H*128 channels, fp32 [B, L] (the statistic of _tp_rms)."""
+    _check4("rms_inv: x", x)
+    B, L = x.shape[:2]
+    inv = torch.empty((B, L), dtype=torch.float32, device=x.device)
+    _rms_call(x, None, eps, None, None, None, inv)
+    return inv
+
+
+@rms_inv.register_fake
+def _(x, eps):
+    return x.new_empty(x.shape[:2], dtype=torch.float32)
+
+
+@torch.library.custom_op("wan_hip::flash_attn_qnorm", mutates_args=())
+def flash_attn_qnorm(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, inv_rms_q: torch.Tensor,
+                     gamma_q: torch.Tensor, cos: Optional[torch.Tensor], sin: Optional[torch.Tensor],
+                     seqlen_k: Optional[torch.Tensor], softmax_scale: float) -> torch.Tensor:
+    """Attention with the query RMSNorm (and RoPE when cos/sin are given) applied in the kernel."""
+    fn = "flash_attn_qnorm"
+    _check_qkv(fn, q, k, v)
+    B, Lq, H, D = q.shape
+    Lk = k.shape[1]
+    _check_vec(fn, "inv_rms_q", inv_rms_q, B * Lq, torch.float32, q.device)
+    _check_vec(fn, "gamma_q", gamma_q, H * D, torch.bfloat16, q.device)
+    if (cos is None) != (sin is None):
+        raise ValueError(f"{fn}: give both cos and sin, or neither")
+    if cos is not None:
+        _check_rope(fn, cos, sin, Lq, q.device)
+    sk = _seqlen_ptr(fn, seqlen_k, B, q.device)
+    out = torch.empty((B, Lq, H, D), dtype=q.dtype, device=q.device)
+    with torch.cuda.device(q.device):
+        N.check("wan_flash_attn_qnorm", N.lib().wan_flash_attn_qnorm(
+            N.tensor4(q), N.tensor4(k), N.tensor4(v), N.tensor4(out), B, H, Lq, Lk, D,
+            inv_rms_q.data_ptr(), gamma_q.data_ptr(),
+            None if cos is None else cos.data_ptr(), None if sin is None else sin.data_ptr(),
+            float(softmax_scale), sk, _stream(q.device)))
+    return out
+
+
+@flash_attn_qnorm.register_fake
+def _(q, k, v, inv_rms_q, gamma_q, cos, sin, seqlen_k, softmax_scale):
+    return q.new_empty(q.shape)
