@@ -11,22 +11,29 @@
 //  * S^T = K Q^T on v_mfma_f32_32x32x16_bf16: the key axis is the MFMA row
 //    axis, so each lane holds ONE query row (lane % 32) and 32 of the 64 keys
 //    of a tile.  Row max / row sum are lane-local plus one exchange with the
-//    lane 32 apart; the O rescale factor is a per-lane scalar.
+//    lane 32 apart (v_permlane32_swap); the O rescale factor is a per-lane scalar.
 //  * O^T += V^T P^T on the same MFMA: P^T comes straight out of the S^T
 //    accumulator (bf16-converted, no shuffle); V^T fragments are read from the
 //    natural [key][d] LDS tile with ds_read_b64_tr_b16, which returns 4 keys of
 //    one channel per lane.  The key order inside a 16-key MFMA step is the
 //    accumulator's row order (8*(r/4) + 4*(lane/32) + r%4); P and V use the
 //    same order, and a contraction index may be permuted freely.
-//  * fp32 online softmax in base 2: exp2(s * scale*log2(e) - m).
-//  * K/V tiles of 64 keys are double-buffered in LDS; the next tile's global
-//    loads are issued before the current tile's MFMAs and land in the other
-//    buffer afterwards (one barrier per tile).
+//  * fp32 online softmax in base 2: exp2(s * scale*log2(e) - m).  The running
+//    max is only moved (and O, l rescaled) when a tile's max exceeds it by more
+//    than kRescaleSlack (in log2 units); otherwise p <= 2^kRescaleSlack and the
+//    stale reference point cancels in O / l exactly.
+//  * K/V tiles of 64 keys go global -> LDS directly (global_load_lds_dwordx4),
+//    double-buffered, 16-byte chunks XOR-swizzled per row so the MFMA operand
+//    reads are bank-conflict free without padding.  Software pipeline: while
+//    the softmax of tile j runs on the VALU, the S^T MFMAs of tile j+1 and the
+//    loads of tiles j+1 (V) and j+2 (K) are in flight.  One barrier per tile.
 //  * Q is loaded once per wave into registers; QK-RMSNorm (given the per-token
 //    inverse RMS) and the 3D-RoPE rotation are applied there, with the
 //    reference's bf16 rounding points (models/fast_dit.py:145-146,169).
 //  * Workgroup ids are remapped so each XCD owns contiguous query blocks of the
 //    same heads (K/V reuse in that XCD's L2).
+#include <stdlib.h>
+
 #include "common.h"
 
 namespace wan {
@@ -35,9 +42,9 @@ namespace {
 
 constexpr int BN = 64;                  // keys per tile
 constexpr int D = kHeadDim;             // 128
-constexpr int KP = D + 8;               // K tile pitch: 272 B rows, 16 rows of a b128 read hit distinct banks
-constexpr int VP = D + 32;              // V tile pitch: 320 B rows, 4 rows of a tr read hit distinct banks
+constexpr int kTileElems = BN * D;      // one K or V tile: 64 rows of 256 B
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kRescaleSlack = 8.0f;   // p <= 256 between rescales
 
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
@@ -50,6 +57,24 @@ __device__ __forceinline__ i16x4 lds_read_tr(const bf16* p) {
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// max / sum of a lane's value and the value of the lane 32 apart (same query row)
+__device__ __forceinline__ float pair_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// LDS tile layouts (element offsets).  Row r = key, 16 chunks of 8 channels.
+//  K: chunk c of row r sits at position c ^ (r & 15): the 16 rows read by a
+//     b128 phase land on 16 distinct bank groups.
+//  V: chunk c of row r sits at position c ^ 4*(r & 3): the 4 rows x 4 chunks
+//     of a transposed-read phase land on 16 distinct bank groups.
+__device__ __forceinline__ int k_swz(int row) { return row & 15; }
+__device__ __forceinline__ int v_swz(int row) { return (row & 3) << 2; }
 
 // Query fragment for the B operand of S^T = K Q^T: lane (n32, hh) holds, for
 // k-step ks, channels 16*ks + 8*hh .. +7 of query row `row`.
@@ -96,18 +121,66 @@ __device__ __forceinline__ void load_q_fragment(const FlashArgs& a, int b, int h
   }
 }
 
+template <int NW>
+struct TileLoader {
+  // Wave `wave` issues the 1 KB blocks i = wave, wave + NW, ... of a 16 KB
+  // tile; lane l fills LDS row 4i + l/16, position l%16.
+  static constexpr int kPerWave = 16 / NW;
+  const bf16* base;         // (batch, head) origin of the K or V tensor
+  int64_t stride;           // token stride (elements)
+  int src_col[kPerWave];    // element column of the chunk this lane fetches
+  int row_in[kPerWave];     // tile row this lane fetches
+  int lane_off[kPerWave];   // row_in * stride + src_col
+
+  __device__ void init(const bf16* b, int64_t st, int wave, int lane, bool is_k) {
+    base = b;
+    stride = st;
+#pragma unroll
+    for (int u = 0; u < kPerWave; ++u) {
+      const int i = wave + NW * u;
+      const int row = 4 * i + (lane >> 4);
+      const int pos = lane & 15;
+      row_in[u] = row;
+      src_col[u] = (pos ^ (is_k ? k_swz(row) : v_swz(row))) * 8;
+      lane_off[u] = row * (int)st + src_col[u];
+    }
+  }
+
+  // Issue the loads of tile t (keys t*BN ..) into `dst`.  In the last tile,
+  // rows past len-1 repeat key len-1 (finite data whose scores are masked).
+  __device__ __forceinline__ void issue(int t, int len, bf16* dst, int wave) const {
+    const int k0 = t * BN;
+    if (k0 + BN <= len) {
+      const bf16* tb = base + (int64_t)k0 * stride;
+#pragma unroll
+      for (int u = 0; u < kPerWave; ++u)
+        __builtin_amdgcn_global_load_lds(tb + lane_off[u], dst + (wave + NW * u) * 512, 16, 0, 0);
+    } else {
+#pragma unroll
+      for (int u = 0; u < kPerWave; ++u) {
+        const int key = min(k0 + row_in[u], len - 1);
+        __builtin_amdgcn_global_load_lds(base + (int64_t)key * stride + src_col[u],
+                                         dst + (wave + NW * u) * 512, 16, 0, 0);
+      }
+    }
+  }
+};
+
 template <int NW, int QP>
 __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a) {
-  constexpr int NT = NW * 64;
   constexpr int BM = NW * 32;
-  constexpr int CHUNKS = BN * D / 8 / NT;  // 16-byte chunks per thread per tile per tensor
-  static_assert(CHUNKS * NT * 8 == BN * D, "tile must split evenly over the workgroup");
 
-  __shared__ __attribute__((aligned(16))) bf16 k_lds[2][BN * KP];
-  __shared__ __attribute__((aligned(16))) bf16 v_lds[2][BN * VP];
+  // Four distinct LDS objects (not one array) so the compiler can prove that
+  // the asynchronous global->LDS writes into one buffer do not alias the
+  // operand reads from the other, and does not wait for them.
+  __shared__ __attribute__((aligned(1024))) bf16 k_lds0[kTileElems];
+  __shared__ __attribute__((aligned(1024))) bf16 k_lds1[kTileElems];
+  __shared__ __attribute__((aligned(1024))) bf16 v_lds0[kTileElems];
+  __shared__ __attribute__((aligned(1024))) bf16 v_lds1[kTileElems];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n32 = lane & 31, hh = lane >> 5;
 
   const int num_m = (a.Lq + BM - 1) / BM;
@@ -121,130 +194,139 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
   const int ntiles = (len + BN - 1) / BN;
 
   const int qrow = mblk * BM + wave * 32 + n32;
-  bf16x8 qf[8];
-  load_q_fragment<QP>(a, b, h, qrow, hh, qf);
-
-  const bf16* kbase = a.k.ptr + b * a.k.sb + h * a.k.sh;
-  const bf16* vbase = a.v.ptr + b * a.v.sb + h * a.v.sh;
-
-  uint4 kr[CHUNKS], vr[CHUNKS];
-  auto gload = [&](int t) {
-#pragma unroll
-    for (int j = 0; j < CHUNKS; ++j) {
-      const int c = tid + NT * j;
-      const int row = c >> 4, col = (c & 15) * 8;
-      const int key = t * BN + row;
-      if (key < len) {
-        kr[j] = *reinterpret_cast<const uint4*>(kbase + (int64_t)key * a.k.st + col);
-        vr[j] = *reinterpret_cast<const uint4*>(vbase + (int64_t)key * a.v.st + col);
-      } else {
-        kr[j] = uint4{0, 0, 0, 0};
-        vr[j] = uint4{0, 0, 0, 0};
-      }
-    }
-  };
-  auto lstore = [&](int buf) {
-#pragma unroll
-    for (int j = 0; j < CHUNKS; ++j) {
-      const int c = tid + NT * j;
-      const int row = c >> 4, col = (c & 15) * 8;
-      *reinterpret_cast<uint4*>(&k_lds[buf][row * KP + col]) = kr[j];
-      *reinterpret_cast<uint4*>(&v_lds[buf][row * VP + col]) = vr[j];
-    }
-  };
-
   f32x16 o[4];
 #pragma unroll
   for (int md = 0; md < 4; ++md) o[md] = f32x16{};
-  float m_run = -INFINITY;  // running max, in scale*log2(e) units
+  float m_run = -INFINITY;  // running reference max, in scale*log2(e) units
   float l_run = 0.f;        // this lane's partial row sum (its 32 keys of each tile)
-  const float sl2 = a.scale * kLog2e;
-
-  // Source lane of a transposed V read: key row (lane%16)/4 of a 4-key group,
-  // channels 4*(lane%4) .. +3 of a 16-channel group.
-  const int tr_key = 4 * hh + ((lane & 15) >> 2);
-  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
   if (ntiles > 0) {
-    gload(0);
-    lstore(0);
-  }
-  __syncthreads();
+    bf16x8 qf[8];
+    load_q_fragment<QP>(a, b, h, qrow, hh, qf);
 
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < ntiles) gload(t + 1);
-    const bf16* Kt = k_lds[buf];
-    const bf16* Vt = v_lds[buf];
+    TileLoader<NW> kl, vl;
+    kl.init(a.k.ptr + b * a.k.sb + h * a.k.sh, a.k.st, wave, lane, true);
+    vl.init(a.v.ptr + b * a.v.sb + h * a.v.sh, a.v.st, wave, lane, false);
 
-    // S^T[key][query] for keys 0..31 (s0) and 32..63 (s1) of this tile.
-    f32x16 s0 = f32x16{}, s1 = f32x16{};
+    const float sl2 = a.scale * kLog2e;
+
+    // lane-constant LDS operand offsets (elements)
+    int k_rd[2][8];
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(Kt + n32 * KP + 16 * ks + 8 * hh);
-      const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(Kt + (32 + n32) * KP + 16 * ks + 8 * hh);
-      s0 = mfma32(a0, qf[ks], s0);
-      s1 = mfma32(a1, qf[ks], s1);
-    }
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        const int row = 32 * mb + n32;
+        k_rd[mb][ks] = row * D + (((2 * ks + hh) ^ k_swz(row)) << 3);
+      }
+    const int tr_row = 4 * hh + ((lane & 15) >> 2);  // + 16*ksp + 8*r
+    const int tr_chunk = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);  // + 4*md
+    const int tr_sub = 4 * (lane & 1);
+    const int tr_x = v_swz(tr_row);  // (row & 3) is the same for every ksp, r
+    int v_rd[4];
+#pragma unroll
+    for (int md = 0; md < 4; ++md) v_rd[md] = tr_row * D + (((4 * md + tr_chunk) ^ tr_x) << 3) + tr_sub;
 
-    const int kt = t * BN;
-    if (kt + BN > len) {
+    auto qk = [&](const bf16* Kt, f32x16& s0, f32x16& s1) {
+      s0 = f32x16{};
+      s1 = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(Kt + k_rd[0][ks]);
+        const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(Kt + k_rd[1][ks]);
+        s0 = mfma32(a0, qf[ks], s0);
+        s1 = mfma32(a1, qf[ks], s1);
+      }
+    };
+
+    // softmax of one S^T tile (keys kt..kt+63) and O += V^T P^T
+    auto softmax_pv = [&](f32x16 s0, f32x16 s1, const bf16* Vt, int kt, bool masked) {
+      if (masked) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kt + 8 * (r >> 2) + 4 * hh + (r & 3);
+          if (key >= len) s0[r] = -INFINITY;
+          if (key + 32 >= len) s1[r] = -INFINITY;
+        }
+      }
+      float mx = fmaxf(s0[0], s0[1]);
+#pragma unroll
+      for (int r = 2; r < 16; ++r) mx = fmaxf(mx, s0[r]);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s1[r]);
+      const float mt = pair_max(mx) * sl2;
+      if (__builtin_amdgcn_ballot_w64(mt > m_run + kRescaleSlack) != 0) {
+        const float m_new = fmaxf(m_run, mt);
+        const float alpha = fast_exp2(m_run - m_new);
+        m_run = m_new;
+        l_run *= alpha;
+#pragma unroll
+        for (int md = 0; md < 4; ++md) o[md] *= alpha;
+      }
+      bf16x8 pb[4];
+      float rs0 = 0.f, rs1 = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int key = kt + 8 * (r >> 2) + 4 * hh + (r & 3);
-        if (key >= len) s0[r] = -INFINITY;
-        if (key + 32 >= len) s1[r] = -INFINITY;
+        const float p0 = fast_exp2(fmaf(s0[r], sl2, -m_run));
+        const float p1 = fast_exp2(fmaf(s1[r], sl2, -m_run));
+        rs0 += p0;
+        rs1 += p1;
+        pb[r >> 3][r & 7] = (bf16)p0;
+        pb[2 + (r >> 3)][r & 7] = (bf16)p1;
       }
-    }
-
-    float mx = s0[0];
+      l_run += rs0 + rs1;
 #pragma unroll
-    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s0[r]);
+      for (int ksp = 0; ksp < 4; ++ksp) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s1[r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx * sl2);
-    const float alpha = fast_exp2(m_run - m_new);
-    m_run = m_new;
-
-    bf16x8 pb[4];
-    float rs = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float p = fast_exp2(fmaf(s0[r], sl2, -m_new));
-      rs += p;
-      pb[r >> 3][r & 7] = (bf16)p;
-    }
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float p = fast_exp2(fmaf(s1[r], sl2, -m_new));
-      rs += p;
-      pb[2 + (r >> 3)][r & 7] = (bf16)p;
-    }
-    l_run = l_run * alpha + rs;
-#pragma unroll
-    for (int md = 0; md < 4; ++md) o[md] *= alpha;
-
-    // O^T[d][query] += V^T[d][key] P^T[key][query], 16 keys per step.
-#pragma unroll
-    for (int ksp = 0; ksp < 4; ++ksp) {
-#pragma unroll
-      for (int md = 0; md < 4; ++md) {
-        const bf16* vp = Vt + (16 * ksp + tr_key) * VP + 32 * md + tr_col;
-        const i16x4 lo = lds_read_tr(vp);
-        const i16x4 hi = lds_read_tr(vp + 8 * VP);
-        const bf16x8 av = __builtin_bit_cast(
-            bf16x8, (short __attribute__((ext_vector_type(8)))){lo[0], lo[1], lo[2], lo[3],
-                                                                hi[0], hi[1], hi[2], hi[3]});
-        o[md] = mfma32(av, pb[ksp], o[md]);
+        for (int md = 0; md < 4; ++md) {
+          const bf16* vp = Vt + 16 * ksp * D + v_rd[md];
+          const i16x4 lo = lds_read_tr(vp);
+          const i16x4 hi = lds_read_tr(vp + 8 * D);
+          const bf16x8 av = __builtin_bit_cast(
+              bf16x8, (short __attribute__((ext_vector_type(8)))){lo[0], lo[1], lo[2], lo[3],
+                                                                  hi[0], hi[1], hi[2], hi[3]});
+          o[md] = mfma32(av, pb[ksp], o[md]);
+        }
       }
-    }
+    };
 
-    if (t + 1 < ntiles) lstore(buf ^ 1);
+    // One pipelined step on tile t (not the last tile): the loads of K(t+2)
+    // and V(t+1), S(t+1) = K(t+1) Q^T, then softmax(S(t)) and O += V(t) P(t).
+    // Tile t lives in buffers t%2; the buffer arguments are static per call.
+    auto step = [&](int t, bf16* k_fill, bf16* v_fill, const bf16* k_next, const bf16* v_cur,
+                    f32x16& c0, f32x16& c1, f32x16& n0, f32x16& n1) {
+      if (t + 2 < ntiles) kl.issue(t + 2, len, k_fill, wave);
+      vl.issue(t + 1, len, v_fill, wave);
+      qk(k_next, n0, n1);
+      softmax_pv(c0, c1, v_cur, t * BN, false);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+    };
+
+    // prologue: K0, V0 (and K1) -> S(0)
+    kl.issue(0, len, k_lds0, wave);
+    vl.issue(0, len, v_lds0, wave);
+    if (ntiles > 1) kl.issue(1, len, k_lds1, wave);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    f32x16 sa0, sa1, sb0, sb1;
+    qk(k_lds0, sa0, sa1);
+    __syncthreads();  // every wave is done with K0 before K2 overwrites it
+
+    int t = 0;
+    for (; t + 2 < ntiles; t += 2) {
+      step(t, k_lds0, v_lds1, k_lds1, v_lds0, sa0, sa1, sb0, sb1);
+      step(t + 1, k_lds1, v_lds0, k_lds0, v_lds1, sb0, sb1, sa0, sa1);
+    }
+    if (t + 1 < ntiles) {  // tiles t (full) and t + 1 (last) remain
+      step(t, k_lds0, v_lds1, k_lds1, v_lds0, sa0, sa1, sb0, sb1);
+      softmax_pv(sb0, sb1, v_lds1, (t + 1) * BN, (t + 2) * BN > len);
+    } else {               // tile t is the last
+      softmax_pv(sa0, sa1, v_lds0, t * BN, (t + 1) * BN > len);
+    }
   }
 
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float l_tot = pair_sum(l_run);
   const float inv_l = l_tot > 0.f ? 1.f / l_tot : 0.f;
   if (qrow < a.Lq) {
     bf16* op = a.o + b * a.o_sb + (int64_t)qrow * a.o_st + h * a.o_sh;
@@ -261,6 +343,15 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
   }
 }
 
+// Explicit instantiations: without them clang emits the host launch stubs of
+// only some of these (lambda-using) kernel template instances.
+template __global__ void flash_fwd_kernel<4, kQPlain>(const FlashArgs);
+template __global__ void flash_fwd_kernel<4, kQNorm>(const FlashArgs);
+template __global__ void flash_fwd_kernel<4, kQNormRope>(const FlashArgs);
+template __global__ void flash_fwd_kernel<8, kQPlain>(const FlashArgs);
+template __global__ void flash_fwd_kernel<8, kQNorm>(const FlashArgs);
+template __global__ void flash_fwd_kernel<8, kQNormRope>(const FlashArgs);
+
 template <int NW, int QP>
 int launch_nw_qp(const FlashArgs& a, hipStream_t s) {
   constexpr int BM = NW * 32;
@@ -272,16 +363,32 @@ int launch_nw_qp(const FlashArgs& a, hipStream_t s) {
   return e == hipSuccess ? 0 : set_error(4, "flash_fwd launch: %s", hipGetErrorString(e));
 }
 
+// Waves per workgroup (query rows per workgroup = 32 * waves): 8 (one
+// 256-row workgroup per CU, K/V tiles shared by all 8 waves; measured faster
+// at L=7854) unless WAN_FLASH_WAVES=4 (two 128-row workgroups per CU).
+int waves_per_workgroup() {
+  static const int w = [] {
+    const char* e = getenv("WAN_FLASH_WAVES");
+    return (e && atoi(e) == 4) ? 4 : 8;
+  }();
+  return w;
+}
+
+template <int NW>
+int launch_nw(const FlashArgs& a, hipStream_t s) {
+  switch (a.qprep) {
+    case kQPlain: return launch_nw_qp<NW, kQPlain>(a, s);
+    case kQNorm: return launch_nw_qp<NW, kQNorm>(a, s);
+    case kQNormRope: return launch_nw_qp<NW, kQNormRope>(a, s);
+    default: return set_error(1, "flash_fwd: unknown q preparation %d", a.qprep);
+  }
+}
+
 }  // namespace
 
 int launch_flash_fwd(const FlashArgs& a, hipStream_t s) {
   if (a.B == 0 || a.H == 0 || a.Lq == 0) return 0;
-  switch (a.qprep) {
-    case kQPlain: return launch_nw_qp<4, kQPlain>(a, s);
-    case kQNorm: return launch_nw_qp<4, kQNorm>(a, s);
-    case kQNormRope: return launch_nw_qp<4, kQNormRope>(a, s);
-    default: return set_error(1, "flash_fwd: unknown q preparation %d", a.qprep);
-  }
+  return waves_per_workgroup() == 8 ? launch_nw<8>(a, s) : launch_nw<4>(a, s);
 }
 
 }  // namespace wan
