@@ -36,6 +36,7 @@
 
 #include "common.h"
 
+
 namespace wan {
 
 namespace {
@@ -124,31 +125,35 @@ __device__ __forceinline__ void load_q_fragment(const FlashArgs& a, int b, int h
 template <int NW>
 struct TileLoader {
   // Wave `wave` issues the 1 KB blocks i = wave, wave + NW, ... of a 16 KB
-  // tile; lane l fills LDS row 4i + l/16, position l%16.
+  // tile; lane l fills LDS row 4i + l/16, position l%16, with the chunk that
+  // the row's swizzle puts there.
   static constexpr int kPerWave = 16 / NW;
   const bf16* base;         // (batch, head) origin of the K or V tensor
   int64_t stride;           // token stride (elements)
-  int src_col[kPerWave];    // element column of the chunk this lane fetches
-  int row_in[kPerWave];     // tile row this lane fetches
-  int lane_off[kPerWave];   // row_in * stride + src_col
+  int lane_off[kPerWave];   // row * stride + source column, for a full tile
+  bool is_k;
 
-  __device__ void init(const bf16* b, int64_t st, int wave, int lane, bool is_k) {
+  __device__ __forceinline__ int row_of(int wave, int lane, int u) const {
+    return 4 * (wave + NW * u) + (lane >> 4);
+  }
+  __device__ __forceinline__ int col_of(int row, int lane) const {
+    return ((lane & 15) ^ (is_k ? k_swz(row) : v_swz(row))) * 8;
+  }
+
+  __device__ void init(const bf16* b, int64_t st, int wave, int lane, bool k) {
     base = b;
     stride = st;
+    is_k = k;
 #pragma unroll
     for (int u = 0; u < kPerWave; ++u) {
-      const int i = wave + NW * u;
-      const int row = 4 * i + (lane >> 4);
-      const int pos = lane & 15;
-      row_in[u] = row;
-      src_col[u] = (pos ^ (is_k ? k_swz(row) : v_swz(row))) * 8;
-      lane_off[u] = row * (int)st + src_col[u];
+      const int row = row_of(wave, lane, u);
+      lane_off[u] = row * (int)st + col_of(row, lane);
     }
   }
 
   // Issue the loads of tile t (keys t*BN ..) into `dst`.  In the last tile,
   // rows past len-1 repeat key len-1 (finite data whose scores are masked).
-  __device__ __forceinline__ void issue(int t, int len, bf16* dst, int wave) const {
+  __device__ __forceinline__ void issue(int t, int len, bf16* dst, int wave, int lane) const {
     const int k0 = t * BN;
     if (k0 + BN <= len) {
       const bf16* tb = base + (int64_t)k0 * stride;
@@ -158,8 +163,9 @@ struct TileLoader {
     } else {
 #pragma unroll
       for (int u = 0; u < kPerWave; ++u) {
-        const int key = min(k0 + row_in[u], len - 1);
-        __builtin_amdgcn_global_load_lds(base + (int64_t)key * stride + src_col[u],
+        const int row = row_of(wave, lane, u);
+        const int key = min(k0 + row, len - 1);
+        __builtin_amdgcn_global_load_lds(base + (int64_t)key * stride + col_of(row, lane),
                                          dst + (wave + NW * u) * 512, 16, 0, 0);
       }
     }
@@ -211,14 +217,10 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
     const float sl2 = a.scale * kLog2e;
 
     // lane-constant LDS operand offsets (elements)
-    int k_rd[2][8];
+    // rows n32 and 32 + n32 share the swizzle (row & 15): one offset per k-step
+    int k_rd[8];
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
-        const int row = 32 * mb + n32;
-        k_rd[mb][ks] = row * D + (((2 * ks + hh) ^ k_swz(row)) << 3);
-      }
+    for (int ks = 0; ks < 8; ++ks) k_rd[ks] = n32 * D + (((2 * ks + hh) ^ k_swz(n32)) << 3);
     const int tr_row = 4 * hh + ((lane & 15) >> 2);  // + 16*ksp + 8*r
     const int tr_chunk = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);  // + 4*md
     const int tr_sub = 4 * (lane & 1);
@@ -232,15 +234,16 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
       s1 = f32x16{};
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) {
-        const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(Kt + k_rd[0][ks]);
-        const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(Kt + k_rd[1][ks]);
+        const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(Kt + k_rd[ks]);
+        const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(Kt + k_rd[ks] + 32 * D);
         s0 = mfma32(a0, qf[ks], s0);
         s1 = mfma32(a1, qf[ks], s1);
       }
     };
 
-    // softmax of one S^T tile (keys kt..kt+63) and O += V^T P^T
-    auto softmax_pv = [&](f32x16 s0, f32x16 s1, const bf16* Vt, int kt, bool masked) {
+    // Masks keys >= len (last tile only), takes the row max and, when it
+    // exceeds the reference max by more than the slack, rescales O and l.
+    auto row_max = [&](f32x16& s0, f32x16& s1, int kt, bool masked) {
       if (masked) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -263,6 +266,10 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
 #pragma unroll
         for (int md = 0; md < 4; ++md) o[md] *= alpha;
       }
+    };
+
+    // P = exp2(S*scale*log2e - m) in bf16, l += sum(P), O^T += V^T P^T
+    auto exp_pv = [&](const f32x16& s0, const f32x16& s1, const bf16* Vt) {
       bf16x8 pb[4];
       float rs0 = 0.f, rs1 = 0.f;
 #pragma unroll
@@ -291,22 +298,24 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
     };
 
     // One pipelined step on tile t (not the last tile): the loads of K(t+2)
-    // and V(t+1), S(t+1) = K(t+1) Q^T, then softmax(S(t)) and O += V(t) P(t).
-    // Tile t lives in buffers t%2; the buffer arguments are static per call.
+    // and V(t+1); the row max of S(t); the MFMAs of S(t+1) = K(t+1) Q^T, then
+    // exp/convert/sum of S(t) and O += V(t) P(t).  Tile t lives in buffers t%2; the buffer
+    // arguments are static per call.
     auto step = [&](int t, bf16* k_fill, bf16* v_fill, const bf16* k_next, const bf16* v_cur,
                     f32x16& c0, f32x16& c1, f32x16& n0, f32x16& n1) {
-      if (t + 2 < ntiles) kl.issue(t + 2, len, k_fill, wave);
-      vl.issue(t + 1, len, v_fill, wave);
+      if (t + 2 < ntiles) kl.issue(t + 2, len, k_fill, wave, lane);
+      vl.issue(t + 1, len, v_fill, wave, lane);
+      row_max(c0, c1, t * BN, false);
       qk(k_next, n0, n1);
-      softmax_pv(c0, c1, v_cur, t * BN, false);
+      exp_pv(c0, c1, v_cur);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
     };
 
     // prologue: K0, V0 (and K1) -> S(0)
-    kl.issue(0, len, k_lds0, wave);
-    vl.issue(0, len, v_lds0, wave);
-    if (ntiles > 1) kl.issue(1, len, k_lds1, wave);
+    kl.issue(0, len, k_lds0, wave, lane);
+    vl.issue(0, len, v_lds0, wave, lane);
+    if (ntiles > 1) kl.issue(1, len, k_lds1, wave, lane);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     f32x16 sa0, sa1, sb0, sb1;
@@ -320,9 +329,11 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
     }
     if (t + 1 < ntiles) {  // tiles t (full) and t + 1 (last) remain
       step(t, k_lds0, v_lds1, k_lds1, v_lds0, sa0, sa1, sb0, sb1);
-      softmax_pv(sb0, sb1, v_lds1, (t + 1) * BN, (t + 2) * BN > len);
+      row_max(sb0, sb1, (t + 1) * BN, (t + 2) * BN > len);
+      exp_pv(sb0, sb1, v_lds1);
     } else {               // tile t is the last
-      softmax_pv(sa0, sa1, v_lds0, t * BN, (t + 1) * BN > len);
+      row_max(sa0, sa1, t * BN, (t + 1) * BN > len);
+      exp_pv(sa0, sa1, v_lds0);
     }
   }
 
