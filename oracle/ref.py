@@ -20,6 +20,9 @@ when given bf16 tensors and without them when given fp32 tensors:
   self_attn_path     models/fast_dit.py:281-292
   cross_attn_path    models/fast_dit.py:297-304
   brute_attention    scripts/validate/attn_bench.py:54-60 (per-head loop), float64 numpy
+  block_forward      scripts/validate/ref_fp32.py:37-59 (one WanAttentionBlock, fp32)
+  dit_forward        scripts/validate/ref_fp32.py:62-99 (CFG noise prediction, fp32)
+  unpatchify         wan/modules/model.py:496-519
 
 Each function is pinned by tests/test_oracle.py (closed forms, invariants,
 library routines and float64 brute force); see that file's header.
@@ -212,3 +215,109 @@ def rel_rms(y: torch.Tensor, ref: torch.Tensor) -> float:
     y = y.double()
     ref = ref.double()
     return float((y - ref).pow(2).mean().sqrt() / ref.pow(2).mean().sqrt())
+
+
+# ---------------------------------------------------------------------------
+# block and DiT forward in fp32 (scripts/validate/ref_fp32.py:20-109)
+# ---------------------------------------------------------------------------
+
+def _rms32(x, norm):
+    return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + norm.eps) * norm.weight.float()
+
+
+def _lin32(x, m):
+    return F.linear(x, m.weight.float(), None if m.bias is None else m.bias.float())
+
+
+def _ln32(x, ln):
+    w = None if ln.weight is None else ln.weight.float()
+    b = None if ln.bias is None else ln.bias.float()
+    return F.layer_norm(x, (x.shape[-1],), w, b, eps=ln.eps)
+
+
+def block_forward(blk, x, e0, cos, sin, ck, cv, num_frames):
+    """One WanAttentionBlock in fp32 with exact SDPA (ref_fp32.py:37-59).
+
+    blk: a module with the WanAttentionBlock parameter names; x [B, L, C]; e0 [1, F, 6, C];
+    cos/sin [L, d/2]; ck/cv [B, Lc, n, d].  All arithmetic in fp32.
+    """
+    sa, ca = blk.self_attn, blk.cross_attn
+    B, L, C = x.shape
+    n, d = sa.num_heads, sa.head_dim
+    x = x.float()
+    e = [t.squeeze(2) for t in (blk.modulation.float().unsqueeze(0) + e0.float()).chunk(6, dim=2)]
+
+    def per_frame(t):
+        return t.view(B, num_frames, L // num_frames, C)
+
+    def mod(h, shift, scale):
+        return (per_frame(h) * (1 + scale.unsqueeze(2)) + shift.unsqueeze(2)).view(B, L, C)
+
+    def gate(y, g):
+        return (per_frame(y) * g.unsqueeze(2)).view(B, L, C)
+
+    def attn(q, k, v):
+        return F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2),
+                                              v.transpose(1, 2)).transpose(1, 2)
+
+    h = mod(_ln32(x, blk.norm1), e[0], e[1])
+    q = rope(_rms32(_lin32(h, sa.q), sa.norm_q).view(B, L, n, d), cos, sin)
+    k = rope(_rms32(_lin32(h, sa.k), sa.norm_k).view(B, L, n, d), cos, sin)
+    v = _lin32(h, sa.v).view(B, L, n, d)
+    x = x + gate(_lin32(attn(q, k, v).reshape(B, L, C), sa.o), e[2])
+    h = _ln32(x, blk.norm3)
+    q = _rms32(_lin32(h, ca.q), ca.norm_q).view(B, L, n, d)
+    x = x + _lin32(attn(q, ck.float(), cv.float()).reshape(B, L, C), ca.o)
+    h = mod(_ln32(x, blk.norm2), e[3], e[4])
+    y = _lin32(F.gelu(_lin32(h, blk.ffn[0]), approximate="tanh"), blk.ffn[2])
+    return x + gate(y, e[5])
+
+
+def sinusoidal_embedding_1d(dim: int, position: torch.Tensor) -> torch.Tensor:
+    """wan/modules/model.py:15-25, float64."""
+    half = dim // 2
+    position = position.type(torch.float64)
+    s = torch.outer(position, torch.pow(10000, -torch.arange(half).to(position).div(half)))
+    return torch.cat([torch.cos(s), torch.sin(s)], dim=1)
+
+
+def dit_forward(model, latent, t, ctx_cond, ctx_null, grid, guide_scale):
+    """CFG noise prediction of the whole DiT in fp32 (ref_fp32.py:62-99): latent [C, F, H, W],
+    contexts [1, Lc, text_dim] -> [C_out, F, H, W]."""
+    f, h, w = grid
+    L = f * h * w
+    dim, heads = model.dim, model.num_heads
+    d = dim // heads
+    cos, sin = rope_tables(model.freqs, grid, d)
+    t_frames = torch.full((f,), float(t), dtype=torch.float64)
+    t_frames[0] = 0.0
+    te = model.time_embedding
+    e = _lin32(F.silu(_lin32(sinusoidal_embedding_1d(model.freq_dim, t_frames).float(), te[0])), te[2])
+    e = e.unsqueeze(0)                                              # [1, F, C]
+    e0 = _lin32(F.silu(e), model.time_projection[1]).unflatten(2, (6, dim))
+    tx = model.text_embedding
+    ctx = torch.cat([ctx_cond, ctx_null], 0).float()
+    context = _lin32(F.gelu(_lin32(ctx, tx[0]), approximate="tanh"), tx[2])
+    pe = model.patch_embedding
+    x = F.conv3d(latent.float().unsqueeze(0), pe.weight.float(), pe.bias.float(), stride=pe.stride)
+    x = x.flatten(2).transpose(1, 2).expand(2, -1, -1).contiguous()
+    for blk in model.blocks:
+        ca = blk.cross_attn
+        ck = _rms32(_lin32(context, ca.k), ca.norm_k).view(2, -1, heads, d)
+        cv = _lin32(context, ca.v).view(2, -1, heads, d)
+        x = block_forward(blk, x, e0, cos, sin, ck, cv, f)
+    hd = model.head
+    m = [t_.squeeze(2) for t_ in (hd.modulation.float().unsqueeze(0) + e.unsqueeze(2)).chunk(2, dim=2)]
+    xn = _ln32(x, hd.norm).view(2, f, L // f, dim)
+    y = _lin32((xn * (1 + m[1].unsqueeze(2)) + m[0].unsqueeze(2)).view(2, L, dim), hd.head)
+    y = unpatchify(y, grid, model.patch_size, model.out_dim)
+    return y[1] + guide_scale * (y[0] - y[1])
+
+
+def unpatchify(y, grid, patch_size, c):
+    """[B, f*h*w, p*q*r*c] -> [B, c, f*p, h*q, w*r], einsum 'fhwpqrc->cfphqwr'
+    (wan/modules/model.py:512-518)."""
+    f, h, w = grid
+    p, q, r = patch_size
+    B = y.shape[0]
+    return y.view(B, f, h, w, p, q, r, c).permute(0, 7, 1, 4, 2, 5, 3, 6).reshape(B, c, f * p, h * q, w * r)

@@ -1,0 +1,94 @@
+"""The flow-matching UniPC sampler (wan2-ti2v-5b_amd/unipc.py) on the CPU.
+
+Pinned by what the mathematics fixes rather than by the reference (whose
+scheduler needs diffusers, absent here):
+  * the sigma / timestep schedule equals its closed form (fm_solvers_unipc.py:115-123,
+    :162-230): shifted linspace, final sigma 0, int64 timesteps;
+  * with the exact flow of a straight path x_s = (1 - s) x0 + s eps (velocity eps - x0),
+    every x0 prediction is exact and the sampler lands on x0 after the last step;
+  * the solver order warms up 1 -> 2 and drops to 1 on the final step.
+"""
+import numpy as np
+import torch
+
+
+def test_schedule_closed_form(W):
+    s = W.unipc.FlowUniPC(num_train_timesteps=1000, shift=1.0)
+    s.set_timesteps(10, shift=5.0)
+    smax, smin = 1.0 - 1.0 / 1000 * 0 - 0.0, None
+    base = 1.0 - np.linspace(1, 1 / 1000, 1000)[::-1]
+    smax, smin = float(np.float32(base[0])), float(np.float32(base[-1]))
+    lin = np.linspace(smax, smin, 11)[:-1]
+    want = 5.0 * lin / (1 + 4.0 * lin)
+    assert np.allclose(s.sigmas[:-1].numpy(), want, rtol=1e-6)
+    assert float(s.sigmas[-1]) == 0.0
+    assert s.timesteps.dtype == torch.int64
+    assert s.timesteps.tolist() == (want * 1000).astype(np.int64).tolist()
+    assert s.timesteps[0] == 999 and bool((s.timesteps[:-1] > s.timesteps[1:]).all())
+
+
+def test_exact_velocity_recovers_x0(W):
+    g = torch.Generator().manual_seed(0)
+    x0 = torch.randn(4, 3, 5, 6, generator=g, dtype=torch.float64)
+    eps = torch.randn(4, 3, 5, 6, generator=g, dtype=torch.float64)
+    s = W.unipc.FlowUniPC(shift=1.0)
+    s.set_timesteps(10, shift=5.0)
+    x = (1 - float(s.sigmas[0])) * x0 + float(s.sigmas[0]) * eps
+    orders = []
+    for _ in range(10):
+        x = s.step(eps - x0, x)
+        orders.append(s.this_order)
+    assert torch.allclose(x, x0, atol=1e-6)
+    assert orders == [1, 2, 2, 2, 2, 2, 2, 2, 2, 1]
+
+
+def test_steps_past_the_schedule_raise(W):
+    s = W.unipc.FlowUniPC()
+    s.set_timesteps(2, shift=5.0)
+    x = torch.zeros(3)
+    s.step(x, x)
+    s.step(x, x)
+    try:
+        s.step(x, x)
+    except RuntimeError:
+        return
+    raise AssertionError("a third step on a 2-step schedule must raise")
+
+
+def _gaussian_flow(s_data):
+    """Exact velocity E[eps - x0 | x_sigma = x] for x0 ~ N(0, s^2), eps ~ N(0, 1), and the std
+    of x_sigma; the ODE dx/dsigma = v carries x along x(sigma) / std(sigma) = const."""
+    def std(sig):
+        return ((1 - sig) ** 2 * s_data ** 2 + sig ** 2) ** 0.5
+
+    def v(x, sig):
+        return x * (sig - (1 - sig) * s_data ** 2) / std(sig) ** 2
+    return v, std
+
+
+def _integrate(W, v, n, shift, x):
+    sched = W.unipc.FlowUniPC(shift=1.0)
+    sched.set_timesteps(n, shift=shift)
+    sig = [float(a) for a in sched.sigmas.double()]
+    xu, xe = x.clone(), x.clone()
+    for i in range(n):
+        xu = sched.step(v(xu, sig[i]), xu)
+        xe = xe + (sig[i + 1] - sig[i]) * v(xe, sig[i])
+    return xu, xe, sig[0]
+
+
+def test_second_order_convergence_on_a_closed_form_ode(W):
+    """A wrong or dropped second-order term leaves first-order convergence: halving the step
+    must cut the UniPC error ~4x (Euler / DDIM: ~2x)."""
+    import math
+    v, std = _gaussian_flow(2.0)
+    x = torch.linspace(-3, 3, 61, dtype=torch.float64)
+    errs = {}
+    for n in (40, 80):
+        xu, xe, s0 = _integrate(W, v, n, 1.0, x)
+        exact = x * std(0.0) / std(s0)
+        errs[n] = (float((xu - exact).abs().max()), float((xe - exact).abs().max()))
+    order_u = math.log2(errs[40][0] / errs[80][0])
+    order_e = math.log2(errs[40][1] / errs[80][1])
+    assert order_u > 1.8 and 0.8 < order_e < 1.2, (order_u, order_e)
+    assert errs[40][0] < errs[40][1] / 50, errs

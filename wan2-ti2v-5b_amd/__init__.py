@@ -7,11 +7,15 @@ Layout of the package:
   ops.py         torch.library custom ops over it (wan_hip::*)
   rope.py        3D-RoPE angle tables (host side, once per grid)
   attention.py   attention() dispatch of wan/modules/attention.py
-  fast_dit.py    the FAST_ATTN_IMPL-selected backends and block span of models/fast_dit.py
+  fast_dit.py    the FAST_ATTN_IMPL-selected backends, the block forward and the batched-CFG
+                 DiT of models/fast_dit.py, and the denoising loop
+  model.py       the WanModel parameter tree (random initialisation for synthetic runs)
+  unipc.py       the flow-matching UniPC sampler that drives the denoising loop
 
 The directory name is not a Python identifier; load it as the module
 `wan2_ti2v_5b_amd` (see load_package() in __graft_entry__.py).
 """
 from . import _native, ops, rope  # noqa: F401
+from . import attention, fast_dit, model, unipc  # noqa: F401
 
-__all__ = ["_native", "ops", "rope"]
+__all__ = ["_native", "ops", "rope", "attention", "fast_dit", "model", "unipc"]
