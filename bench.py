@@ -14,7 +14,9 @@ attention, on seeded N(0,1) projections already resident in HBM.
   cpu_baseline  the oracle's torch SDPA (fp32) on the host cores, on a bounded sample
               of (batch, head) pairs of the same workload
   extra       the same path at L=1080 and the masked cross-attention (Lq=7854,
-              512 text keys, per-sample lengths U[16, 512]), with HBM GB/s
+              512 text keys, per-sample lengths U[16, 512]), with HBM GB/s; one
+              WanAttentionBlock (D) and the 30-layer DiT, 10 UniPC steps (E):
+              dit_s_per_step is the second half of the metric
 
 Prints one JSON line on stdout.  Usage:
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--cpu-seconds S] [--no-cpu-baseline]
@@ -38,6 +40,21 @@ PEAK_HBM_GBS = 8000.0
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+TRAFFIC_PROFILE = os.path.join("profiles", "flash_fwd_selfattn_L7854.md")
+
+
+def profiled_traffic():
+    """HBM bytes per launch of the config C attention kernel, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (calibrated against a plain copy), or None."""
+    import re
+    try:
+        text = open(os.path.join(ROOT, TRAFFIC_PROFILE)).read()
+    except OSError:
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", text, re.M)
+    return int(m.group(1)) if m else None
 
 
 def attn_flops(b, h, lq, lk):
@@ -146,6 +163,64 @@ def bench_cross(torch, W, dev, steps, warmup):
     }
 
 
+def bench_dit(torch, W, dev, steps, layers):
+    """Config D (one WanAttentionBlock at L=7854) and config E (the 30-layer DiT, 10 UniPC
+    steps at 704x544x81) with random bf16 weights (std 0.02) and the HIP attention path."""
+    cfg = W.model.WanConfig()
+    model = W.model.random_model(cfg, num_layers=layers, device=dev, seed=0)
+    fast = W.fast_dit.FastWanDiT(model, GRID_C, cfg.sample_guide_scale, attn_impl="hip", cross_impl="hip")
+    g = torch.Generator().manual_seed(5)
+    f, h, w = GRID_C
+    latent = torch.randn(cfg.in_dim, f, 2 * h, 2 * w, generator=g).to(dev)     # [48, 21, 34, 44]
+    ctx_c = torch.randn(1, cfg.text_len, cfg.text_dim, generator=g).to(dev)
+    ctx_n = torch.randn(1, cfg.text_len, cfg.text_dim, generator=g).to(dev)
+    image_latent = torch.randn(cfg.in_dim, 1, 2 * h, 2 * w, generator=g).to(dev)
+    fast.set_context(ctx_c, ctx_n)
+    out = fast(latent, torch.tensor(999))                    # warm-up (GEMM heuristics, allocator)
+    torch.cuda.synchronize()
+
+    # config D: one block, its inputs as in the DiT
+    e, e0 = fast._time_embed(torch.tensor(500))
+    x = fast.patch(latent)
+    ck, cv = fast.context[0]
+    blk = fast.blocks[0]
+    for _ in range(2):
+        blk(x, e0, fast.cos, fast.sin, ck, cv)
+    e_a, e_b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e_a.record()
+    for _ in range(5):
+        y = blk(x, e0, fast.cos, fast.sin, ck, cv)
+    e_b.record()
+    torch.cuda.synchronize()
+    block_ms = e_a.elapsed_time(e_b) / 5
+    L = x.shape[1]
+    C, Fd = cfg.dim, cfg.ffn_dim
+    block_flops = 2.0 * B * L * (6 * C * C + 2 * C * Fd) + attn_flops(B, H, L, L) + 4.0 * B * H * L * L_TEXT * D
+    del y
+
+    # config E: the denoising loop
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e_a.record()
+    final = W.fast_dit.denoise(fast, latent, steps, cfg.sample_shift, image_latent=image_latent)
+    e_b.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    dit_s = e_a.elapsed_time(e_b) / 1e3
+    finite = bool(torch.isfinite(final.float()).all())
+    step_flops = layers * block_flops
+    return {
+        "block_D": {"workload": "one WanAttentionBlock forward, B=2, L=7854, dim 3072, ffn 14336, "
+                                "24 heads, 512 text keys, random bf16 weights",
+                    "ms": block_ms, "tflops": block_flops / (block_ms * 1e-3) / 1e12},
+        "dit_E": {"workload": f"{layers}-layer Wan2.2-TI2V-5B DiT, {steps} UniPC steps (shift 5.0, guide 5.0), "
+                              "704x544x81 (latent 48x21x34x44, L=7854), CFG batch 2, random bf16 weights",
+                  "s_per_step": dit_s / steps, "wall_s_per_step": wall / steps,
+                  "tflops": step_flops / (dit_s / steps) / 1e12, "finite": finite},
+    }
+
+
 def cpu_baseline(torch, host, seconds):
     """fp32 torch SDPA (the oracle) on the host cores: QK-RMSNorm + RoPE over all tokens,
     then SDPA on (batch, head) pairs until `seconds` of CPU work are done."""
@@ -185,6 +260,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-dit", action="store_true", help="skip the block (D) and 30-layer DiT (E) runs")
+    ap.add_argument("--dit-steps", type=int, default=10)
+    ap.add_argument("--dit-layers", type=int, default=30)
     ap.add_argument("--profile-copy", type=int, default=0, metavar="BYTES",
                     help="only run 10 device-to-device copies of BYTES (HBM counter calibration)")
     args = ap.parse_args()
@@ -236,6 +314,9 @@ def main():
             "tflops_kernel": attn_flops(B, H, LA, LA) / (aA * 1e-3) / 1e12}
         extra["cross_attn"] = bench_cross(torch, W, dev, args.steps, args.warmup)
         log(f"extra: {json.dumps(extra)}")
+    if not args.no_dit:
+        extra.update(bench_dit(torch, W, dev, args.dit_steps, args.dit_layers))
+        log(f"block D: {extra['block_D']['ms']:.2f} ms; DiT E: {extra['dit_E']['s_per_step']:.3f} s/step")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -258,12 +339,14 @@ def main():
         "config": {"workload": "fused QK-RMSNorm + 3D-RoPE + flash self-attention, B=2 (CFG), "
                                "L=7854 (latent 21x17x22, 704x544x81), 24 heads, head_dim 128",
                    "global_batch": B, "seq_len": L, "heads": H, "head_dim": D, "parallelism": "none (1 GPU)"},
-        "roofline": {"kernel": "flash_fwd_kernel<4,2> (attention with in-kernel Q norm + RoPE)",
+        "roofline": {"kernel": "flash_fwd_kernel<8,2> (attention with the Q RMSNorm + RoPE applied in-kernel)",
                      "bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None,
+                     "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS, "traffic": profiled_traffic(),
+                     "traffic_source": TRAFFIC_PROFILE + " (FETCH_SIZE x2.0 + WRITE_SIZE x1.0, per launch)",
                      "kernel_ms": t_attn, "flops_per_launch": flops},
         "cpu_baseline": cpu,
         "prep_ms": t_prep,
+        "dit_s_per_step": extra.get("dit_E", {}).get("s_per_step"),
         "extra": extra,
     }
     print(json.dumps(line), flush=True)
