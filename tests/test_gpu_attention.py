@@ -105,6 +105,35 @@ def test_plain_self_ragged(W, B, Lq, Lk, H, actual):
     assert ref.rel_rms(out, want16) <= TOL_BF16
 
 
+@pytest.mark.parametrize("pattern,actual", [("rising", 0), ("falling", 0), ("jumps", 0), ("jumps", 937)])
+def test_large_logit_swings(W, pattern, actual):
+    """Logits whose level moves by ~10-60 natural units between 64-key tiles (up to ~200:
+    exp overflows without a reference max).  Exercises the exact-max rescale of O and l,
+    which runs only when a tile's sum of p exceeds its bound."""
+    B, Lq, Lk, H = 1, 96, 1000, 2
+    g = torch.Generator().manual_seed(11)
+    q = torch.randn(B, Lq, H, D, generator=g) * 0.3
+    q[..., 0] = 1.0 + 0.1 * torch.randn(B, Lq, H, generator=g)
+    k = torch.randn(B, Lk, H, D, generator=g) * 0.3
+    j = torch.arange(Lk, dtype=torch.float32)
+    if pattern == "rising":
+        level = 0.2 * j
+    elif pattern == "falling":
+        level = -0.2 * j
+    else:
+        level = (torch.rand(Lk // 64 + 1, generator=g) * 120 - 60).repeat_interleave(64)[:Lk]
+    k[..., 0] = (level / SCALE).view(1, Lk, 1)
+    v = torch.randn(B, Lk, H, D, generator=g)
+    q, k, v = q.bfloat16(), k.bfloat16(), v.bfloat16()
+    out = W.ops.flash_self_attn(*_d(q, k, v), SCALE, actual).cpu()
+    n = actual if actual > 0 else Lk
+    want = torch.from_numpy(ref.brute_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                                SCALE, n)).float()
+    e = ref.rel_rms(out, want)
+    print(f"{pattern} actual={actual}: rel_rms vs float64 {e:.3e}")
+    assert torch.isfinite(out.float()).all() and e <= 5e-3
+
+
 def test_single_key_returns_its_value(W):
     q, k, v = _bf((2, 77, 3, D), 1), _bf((2, 9, 3, D), 2), _bf((2, 9, 3, D), 3)
     out = W.ops.flash_self_attn(*_d(q, k, v), SCALE, 1).cpu()

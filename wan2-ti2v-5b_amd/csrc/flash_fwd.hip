@@ -7,7 +7,8 @@
 // like wan_flash_self_attn (kernels/self_attention_nst.py:73-78,715-722), with
 // the per-sample key lengths of the cross-attention call site.
 //
-// Design (one workgroup = NW waves = NW*32 query rows of one (batch, head)):
+// Design (one workgroup = 8 waves = 256 query rows of one (batch, head); one
+// workgroup per CU at 256 VGPRs per wave):
 //  * S^T = K Q^T on v_mfma_f32_32x32x16_bf16: the key axis is the MFMA row
 //    axis, so each lane holds ONE query row (lane % 32) and 32 of the 64 keys
 //    of a tile.  Row max / row sum are lane-local plus one exchange with the
@@ -18,22 +19,26 @@
 //    one channel per lane.  The key order inside a 16-key MFMA step is the
 //    accumulator's row order (8*(r/4) + 4*(lane/32) + r%4); P and V use the
 //    same order, and a contraction index may be permuted freely.
-//  * fp32 online softmax in base 2: exp2(s * scale*log2(e) - m).  The running
-//    max is only moved (and O, l rescaled) when a tile's max exceeds it by more
-//    than kRescaleSlack (in log2 units); otherwise p <= 2^kRescaleSlack and the
-//    stale reference point cancels in O / l exactly.
+//  * fp32 online softmax in base 2: p = exp2(s * scale*log2(e) - m).  The
+//    reference point m is not the exact running max: a tile is exponentiated
+//    against the current m, and only when some lane's sum of the tile's p
+//    exceeds kSumBound (or is inf / NaN) is the tile's exact max taken, m
+//    moved and O, l rescaled (the first tile always; later tiles rarely).
+//    Otherwise every p <= kSumBound and the stale reference point cancels in
+//    O / l exactly.  l sums the bf16-rounded p that the PV MFMAs consume.
 //  * K/V tiles of 64 keys go global -> LDS directly (global_load_lds_dwordx4),
 //    double-buffered, 16-byte chunks XOR-swizzled per row so the MFMA operand
 //    reads are bank-conflict free without padding.  Software pipeline: while
 //    the softmax of tile j runs on the VALU, the S^T MFMAs of tile j+1 and the
 //    loads of tiles j+1 (V) and j+2 (K) are in flight.  One barrier per tile.
+//    In program order the S^T MFMAs of tile j+1 alternate with the exp2 /
+//    convert / sum of tile j (two MFMAs and four exponentials per k-step), and
+//    K and V^T operand fragments are read one MFMA ahead.
 //  * Q is loaded once per wave into registers; QK-RMSNorm (given the per-token
 //    inverse RMS) and the 3D-RoPE rotation are applied there, with the
 //    reference's bf16 rounding points (models/fast_dit.py:145-146,169).
 //  * Workgroup ids are remapped so each XCD owns contiguous query blocks of the
 //    same heads (K/V reuse in that XCD's L2).
-#include <stdlib.h>
-
 #include "common.h"
 
 
@@ -42,10 +47,11 @@ namespace wan {
 namespace {
 
 constexpr int BN = 64;                  // keys per tile
+constexpr int kWaves = 8;               // waves per workgroup: 256 query rows, one workgroup per CU
 constexpr int D = kHeadDim;             // 128
 constexpr int kTileElems = BN * D;      // one K or V tile: 64 rows of 256 B
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kRescaleSlack = 8.0f;   // p <= 256 between rescales
+constexpr float kSumBound = 65536.0f;   // per-lane tile sum of P that forces a rescale
 
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
@@ -126,11 +132,13 @@ template <int NW>
 struct TileLoader {
   // Wave `wave` issues the 1 KB blocks i = wave, wave + NW, ... of a 16 KB
   // tile; lane l fills LDS row 4i + l/16, position l%16, with the chunk that
-  // the row's swizzle puts there.
+  // the row's swizzle puts there.  Full tiles are addressed as a wave-uniform
+  // base plus a 32-bit per-lane byte offset (the scalar-base form of the
+  // load: no 64-bit per-lane address is kept live).
   static constexpr int kPerWave = 16 / NW;
-  const bf16* base;         // (batch, head) origin of the K or V tensor
-  int64_t stride;           // token stride (elements)
-  int lane_off[kPerWave];   // row * stride + source column, for a full tile
+  const char* base;              // (batch, head) origin of the K or V tensor
+  int64_t stride;                // token stride (elements)
+  uint32_t lane_off[kPerWave];   // bytes: row * stride + source column, for a full tile
   bool is_k;
 
   __device__ __forceinline__ int row_of(int wave, int lane, int u) const {
@@ -141,13 +149,13 @@ struct TileLoader {
   }
 
   __device__ void init(const bf16* b, int64_t st, int wave, int lane, bool k) {
-    base = b;
+    base = reinterpret_cast<const char*>(b);
     stride = st;
     is_k = k;
 #pragma unroll
     for (int u = 0; u < kPerWave; ++u) {
       const int row = row_of(wave, lane, u);
-      lane_off[u] = row * (int)st + col_of(row, lane);
+      lane_off[u] = (uint32_t)(row * st + col_of(row, lane)) * 2u;
     }
   }
 
@@ -156,16 +164,21 @@ struct TileLoader {
   __device__ __forceinline__ void issue(int t, int len, bf16* dst, int wave, int lane) const {
     const int k0 = t * BN;
     if (k0 + BN <= len) {
-      const bf16* tb = base + (int64_t)k0 * stride;
+      const char* tb = base + (int64_t)k0 * stride * 2;
 #pragma unroll
-      for (int u = 0; u < kPerWave; ++u)
-        __builtin_amdgcn_global_load_lds(tb + lane_off[u], dst + (wave + NW * u) * 512, 16, 0, 0);
+      for (int u = 0; u < kPerWave; ++u) {
+        // keep the 32 -> 64-bit extension next to the load (not hoisted out of
+        // the tile loop) so instruction selection sees sgpr + zext(vgpr)
+        uint32_t off = lane_off[u];
+        asm volatile("" : "+v"(off));
+        __builtin_amdgcn_global_load_lds(tb + off, dst + (wave + NW * u) * 512, 16, 0, 0);
+      }
     } else {
 #pragma unroll
       for (int u = 0; u < kPerWave; ++u) {
         const int row = row_of(wave, lane, u);
         const int key = min(k0 + row, len - 1);
-        __builtin_amdgcn_global_load_lds(base + (int64_t)key * stride + col_of(row, lane),
+        __builtin_amdgcn_global_load_lds(base + ((int64_t)key * stride + col_of(row, lane)) * 2,
                                          dst + (wave + NW * u) * 512, 16, 0, 0);
       }
     }
@@ -241,10 +254,52 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
       }
     };
 
-    // Masks keys >= len (last tile only), takes the row max and, when it
-    // exceeds the reference max by more than the slack, rescales O and l.
-    auto row_max = [&](f32x16& s0, f32x16& s1, int kt, bool masked) {
-      if (masked) {
+    // P = exp2(S * scale*log2e - m_run) in bf16, and this lane's sum of P
+    // (of the bf16 values the PV MFMAs use; v_dot2 against (1, 1)).
+    auto exp_tile = [&](const f32x16& s0, const f32x16& s1, bf16x8 pb[4]) -> float {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        pb[r >> 3][r & 7] = (bf16)fast_exp2(fmaf(s0[r], sl2, -m_run));
+        pb[2 + (r >> 3)][r & 7] = (bf16)fast_exp2(fmaf(s1[r], sl2, -m_run));
+      }
+      const bf16x2 one = {(bf16)1.0f, (bf16)1.0f};
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[i] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pb[i], pb[i], 0, 1), one, acc[i], false);
+        acc[i] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pb[i], pb[i], 2, 3), one, acc[i], false);
+        acc[i] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pb[i], pb[i], 4, 5), one, acc[i], false);
+        acc[i] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pb[i], pb[i], 6, 7), one, acc[i], false);
+      }
+      return (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    };
+
+    // Completes the softmax numerator of a tile whose P was computed against
+    // the current reference max with lane sum rs.  Only if some lane's sum
+    // exceeds kSumBound (or is inf / NaN: the first tile, where m_run is -inf)
+    // does the wave take the tile's exact row max, rescale O and l, and
+    // exponentiate again; afterwards every p <= 1.
+    auto finish = [&](const f32x16& s0, const f32x16& s1, float rs, bf16x8 pb[4]) {
+      if (__builtin_amdgcn_ballot_w64(!(rs <= kSumBound)) != 0) {
+        float mx = fmaxf(s0[0], s0[1]);
+#pragma unroll
+        for (int r = 2; r < 16; ++r) mx = fmaxf(mx, s0[r]);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s1[r]);
+        const float m_new = fmaxf(m_run, pair_max(mx) * sl2);
+        const float alpha = fast_exp2(m_run - m_new);
+        m_run = m_new;
+        l_run *= alpha;
+#pragma unroll
+        for (int md = 0; md < 4; ++md) o[md] *= alpha;
+        rs = exp_tile(s0, s1, pb);
+      }
+      l_run += rs;
+    };
+
+    // Softmax numerator of the last tile, keys >= len masked.
+    auto softmax_last = [&](f32x16& s0, f32x16& s1, int kt, bf16x8 pb[4]) {
+      if ((kt + BN) > len) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = kt + 8 * (r >> 2) + 4 * hh + (r & 3);
@@ -252,62 +307,77 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
           if (key + 32 >= len) s1[r] = -INFINITY;
         }
       }
-      float mx = fmaxf(s0[0], s0[1]);
-#pragma unroll
-      for (int r = 2; r < 16; ++r) mx = fmaxf(mx, s0[r]);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s1[r]);
-      const float mt = pair_max(mx) * sl2;
-      if (__builtin_amdgcn_ballot_w64(mt > m_run + kRescaleSlack) != 0) {
-        const float m_new = fmaxf(m_run, mt);
-        const float alpha = fast_exp2(m_run - m_new);
-        m_run = m_new;
-        l_run *= alpha;
-#pragma unroll
-        for (int md = 0; md < 4; ++md) o[md] *= alpha;
-      }
+      finish(s0, s1, exp_tile(s0, s1, pb), pb);
     };
 
-    // P = exp2(S*scale*log2e - m) in bf16, l += sum(P), O^T += V^T P^T
-    auto exp_pv = [&](const f32x16& s0, const f32x16& s1, const bf16* Vt) {
-      bf16x8 pb[4];
-      float rs0 = 0.f, rs1 = 0.f;
+    // The MFMAs of S(next) = K Q^T, interleaved in program order with the
+    // exponentials of the current tile's S (c0, c1): per k-step two MFMAs and
+    // elements 2ks, 2ks+1 of each half (4 fma + 4 exp2 + 2 cvt + 2 dot2).  K
+    // fragments are read one k-step ahead.  Returns this lane's sum of P.
+    auto qk_exp = [&](const bf16* Kt, f32x16& n0, f32x16& n1, const f32x16& c0, const f32x16& c1,
+                      bf16x8 pb[4]) -> float {
+      const bf16x2 one = {(bf16)1.0f, (bf16)1.0f};
+      float acc0 = 0.f, acc1 = 0.f;
+      bf16x8 a0 = *reinterpret_cast<const bf16x8*>(Kt + k_rd[0]);
+      bf16x8 a1 = *reinterpret_cast<const bf16x8*>(Kt + k_rd[0] + 32 * D);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p0 = fast_exp2(fmaf(s0[r], sl2, -m_run));
-        const float p1 = fast_exp2(fmaf(s1[r], sl2, -m_run));
-        rs0 += p0;
-        rs1 += p1;
-        pb[r >> 3][r & 7] = (bf16)p0;
-        pb[2 + (r >> 3)][r & 7] = (bf16)p1;
-      }
-      l_run += rs0 + rs1;
-#pragma unroll
-      for (int ksp = 0; ksp < 4; ++ksp) {
-#pragma unroll
-        for (int md = 0; md < 4; ++md) {
-          const bf16* vp = Vt + 16 * ksp * D + v_rd[md];
-          const i16x4 lo = lds_read_tr(vp);
-          const i16x4 hi = lds_read_tr(vp + 8 * D);
-          const bf16x8 av = __builtin_bit_cast(
-              bf16x8, (short __attribute__((ext_vector_type(8)))){lo[0], lo[1], lo[2], lo[3],
-                                                                  hi[0], hi[1], hi[2], hi[3]});
-          o[md] = mfma32(av, pb[ksp], o[md]);
+      for (int ks = 0; ks < 8; ++ks) {
+        bf16x8 b0, b1;
+        if (ks < 7) {
+          b0 = *reinterpret_cast<const bf16x8*>(Kt + k_rd[ks + 1]);
+          b1 = *reinterpret_cast<const bf16x8*>(Kt + k_rd[ks + 1] + 32 * D);
         }
+        n0 = mfma32(a0, qf[ks], ks == 0 ? f32x16{} : n0);
+        n1 = mfma32(a1, qf[ks], ks == 0 ? f32x16{} : n1);
+        const int r = 2 * ks;
+        const bf16x2 u = {(bf16)fast_exp2(fmaf(c0[r], sl2, -m_run)),
+                          (bf16)fast_exp2(fmaf(c0[r + 1], sl2, -m_run))};
+        const bf16x2 w = {(bf16)fast_exp2(fmaf(c1[r], sl2, -m_run)),
+                          (bf16)fast_exp2(fmaf(c1[r + 1], sl2, -m_run))};
+        pb[ks >> 2][2 * (ks & 3)] = u[0];
+        pb[ks >> 2][2 * (ks & 3) + 1] = u[1];
+        pb[2 + (ks >> 2)][2 * (ks & 3)] = w[0];
+        pb[2 + (ks >> 2)][2 * (ks & 3) + 1] = w[1];
+        acc0 = __builtin_amdgcn_fdot2_f32_bf16(u, one, acc0, false);
+        acc1 = __builtin_amdgcn_fdot2_f32_bf16(w, one, acc1, false);
+        if (ks < 7) {
+          a0 = b0;
+          a1 = b1;
+        }
+      }
+      return acc0 + acc1;
+    };
+
+    // O^T += V^T P^T, V^T fragments read one MFMA ahead
+    auto pv = [&](const bf16x8 pb[4], const bf16* Vt) {
+      auto vfrag = [&](int i) -> bf16x8 {
+        const bf16* vp = Vt + 16 * (i >> 2) * D + v_rd[i & 3];
+        const i16x4 lo = lds_read_tr(vp);
+        const i16x4 hi = lds_read_tr(vp + 8 * D);
+        return __builtin_bit_cast(bf16x8, (short __attribute__((ext_vector_type(8)))){
+                                              lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+      };
+      bf16x8 cur = vfrag(0);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        bf16x8 nxt;
+        if (i < 15) nxt = vfrag(i + 1);
+        o[i & 3] = mfma32(cur, pb[i >> 2], o[i & 3]);
+        if (i < 15) cur = nxt;
       }
     };
 
     // One pipelined step on tile t (not the last tile): the loads of K(t+2)
-    // and V(t+1); the row max of S(t); the MFMAs of S(t+1) = K(t+1) Q^T, then
-    // exp/convert/sum of S(t) and O += V(t) P(t).  Tile t lives in buffers t%2; the buffer
-    // arguments are static per call.
+    // and V(t+1); the MFMAs of S(t+1) = K(t+1) Q^T, the softmax of S(t) and
+    // O += V(t) P(t).  Tile t lives in buffers t%2; the buffer arguments are
+    // static per call.
     auto step = [&](int t, bf16* k_fill, bf16* v_fill, const bf16* k_next, const bf16* v_cur,
                     f32x16& c0, f32x16& c1, f32x16& n0, f32x16& n1) {
       if (t + 2 < ntiles) kl.issue(t + 2, len, k_fill, wave, lane);
       vl.issue(t + 1, len, v_fill, wave, lane);
-      row_max(c0, c1, t * BN, false);
-      qk(k_next, n0, n1);
-      exp_pv(c0, c1, v_cur);
+      bf16x8 pb[4];
+      finish(c0, c1, qk_exp(k_next, n0, n1, c0, c1, pb), pb);
+      pv(pb, v_cur);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
     };
@@ -327,13 +397,14 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
       step(t, k_lds0, v_lds1, k_lds1, v_lds0, sa0, sa1, sb0, sb1);
       step(t + 1, k_lds1, v_lds0, k_lds0, v_lds1, sb0, sb1, sa0, sa1);
     }
+    bf16x8 pb[4];
     if (t + 1 < ntiles) {  // tiles t (full) and t + 1 (last) remain
       step(t, k_lds0, v_lds1, k_lds1, v_lds0, sa0, sa1, sb0, sb1);
-      row_max(sb0, sb1, (t + 1) * BN, (t + 2) * BN > len);
-      exp_pv(sb0, sb1, v_lds1);
+      softmax_last(sb0, sb1, (t + 1) * BN, pb);
+      pv(pb, v_lds1);
     } else {               // tile t is the last
-      row_max(sa0, sa1, t * BN, (t + 1) * BN > len);
-      exp_pv(sa0, sa1, v_lds0);
+      softmax_last(sa0, sa1, t * BN, pb);
+      pv(pb, v_lds0);
     }
   }
 
@@ -356,50 +427,31 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
 
 // Explicit instantiations: without them clang emits the host launch stubs of
 // only some of these (lambda-using) kernel template instances.
-template __global__ void flash_fwd_kernel<4, kQPlain>(const FlashArgs);
-template __global__ void flash_fwd_kernel<4, kQNorm>(const FlashArgs);
-template __global__ void flash_fwd_kernel<4, kQNormRope>(const FlashArgs);
-template __global__ void flash_fwd_kernel<8, kQPlain>(const FlashArgs);
-template __global__ void flash_fwd_kernel<8, kQNorm>(const FlashArgs);
-template __global__ void flash_fwd_kernel<8, kQNormRope>(const FlashArgs);
+template __global__ void flash_fwd_kernel<kWaves, kQPlain>(const FlashArgs);
+template __global__ void flash_fwd_kernel<kWaves, kQNorm>(const FlashArgs);
+template __global__ void flash_fwd_kernel<kWaves, kQNormRope>(const FlashArgs);
 
-template <int NW, int QP>
-int launch_nw_qp(const FlashArgs& a, hipStream_t s) {
-  constexpr int BM = NW * 32;
+template <int QP>
+int launch_qp(const FlashArgs& a, hipStream_t s) {
+  constexpr int BM = kWaves * 32;
   const int64_t num_m = (a.Lq + BM - 1) / BM;
   const int64_t grid = num_m * a.B * a.H;
   if (grid > 0x7fffffff) return set_error(2, "flash_fwd: grid of %lld workgroups too large", (long long)grid);
-  hipLaunchKernelGGL((flash_fwd_kernel<NW, QP>), dim3((unsigned)grid), dim3(NW * 64), 0, s, a);
+  hipLaunchKernelGGL((flash_fwd_kernel<kWaves, QP>), dim3((unsigned)grid), dim3(kWaves * 64), 0, s, a);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? 0 : set_error(4, "flash_fwd launch: %s", hipGetErrorString(e));
-}
-
-// Waves per workgroup (query rows per workgroup = 32 * waves): 8 (one
-// 256-row workgroup per CU, K/V tiles shared by all 8 waves; measured faster
-// at L=7854) unless WAN_FLASH_WAVES=4 (two 128-row workgroups per CU).
-int waves_per_workgroup() {
-  static const int w = [] {
-    const char* e = getenv("WAN_FLASH_WAVES");
-    return (e && atoi(e) == 4) ? 4 : 8;
-  }();
-  return w;
-}
-
-template <int NW>
-int launch_nw(const FlashArgs& a, hipStream_t s) {
-  switch (a.qprep) {
-    case kQPlain: return launch_nw_qp<NW, kQPlain>(a, s);
-    case kQNorm: return launch_nw_qp<NW, kQNorm>(a, s);
-    case kQNormRope: return launch_nw_qp<NW, kQNormRope>(a, s);
-    default: return set_error(1, "flash_fwd: unknown q preparation %d", a.qprep);
-  }
 }
 
 }  // namespace
 
 int launch_flash_fwd(const FlashArgs& a, hipStream_t s) {
   if (a.B == 0 || a.H == 0 || a.Lq == 0) return 0;
-  return waves_per_workgroup() == 8 ? launch_nw<8>(a, s) : launch_nw<4>(a, s);
+  switch (a.qprep) {
+    case kQPlain: return launch_qp<kQPlain>(a, s);
+    case kQNorm: return launch_qp<kQNorm>(a, s);
+    case kQNormRope: return launch_qp<kQNormRope>(a, s);
+    default: return set_error(1, "flash_fwd: unknown q preparation %d", a.qprep);
+  }
 }
 
 }  // namespace wan
