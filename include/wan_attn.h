@@ -141,6 +141,27 @@ int wan_flash_attn_qnorm(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor ou
                          const float* rope_cos, const float* rope_sin, float softmax_scale,
                          const int32_t* seqlen_k_dev, void* stream);
 
+/*
+ * One adaLN stage of a WanAttentionBlock (the pointwise work between its
+ * GEMMs), fused into one pass over the residual stream.  With f the frame of
+ * the token (seqlen / frames contiguous tokens per frame) and e[f, i] the
+ * modulation rows:
+ *   r     = x | bf16(x + y) | bf16(x + bf16(y * e[f, gate_idx]))
+ *   x_out = r                                       (written when non-NULL)
+ *   ln    = bf16(LayerNorm(r) [* ln_weight + ln_bias])   fp32 statistics, eps
+ *   h_out = ln | bf16(bf16(ln * bf16(1 + e[f, scale_idx])) + e[f, shift_idx])
+ * Replaces the eager ops of models/fast_dit.py:280 (norm1 + _modulate), :294
+ * (x + _gate(y) then norm3), :306-307 (x + cross output, norm2 + _modulate) and
+ * :311 (x + _gate(y)); _modulate / _gate are :172-181, WanLayerNorm is
+ * wan/modules/model.py:89-99.  x, y, x_out, h_out: [batch, seqlen, dim] bf16
+ * contiguous; e: [frames, 6, dim] bf16 contiguous (block modulation + time
+ * projection, models/fast_dit.py:275-276); indices -1 = absent.  y, x_out,
+ * h_out, e, ln_weight/ln_bias may be NULL as the stage needs.
+ */
+int wan_adaln(const void* x, const void* y, void* x_out, void* h_out, int batch, int seqlen,
+              int dim, const void* e, int frames, int gate_idx, int shift_idx, int scale_idx,
+              const void* ln_weight, const void* ln_bias, float eps, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

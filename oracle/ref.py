@@ -23,6 +23,9 @@ when given bf16 tensors and without them when given fp32 tensors:
   block_forward      scripts/validate/ref_fp32.py:37-59 (one WanAttentionBlock, fp32)
   dit_forward        scripts/validate/ref_fp32.py:62-99 (CFG noise prediction, fp32)
   unpatchify         wan/modules/model.py:496-519
+  adaln              models/fast_dit.py:172-181,280,294,306-311 with WanLayerNorm
+                     (wan/modules/model.py:89-99): one bf16 adaLN stage of a block
+  layer_norm64       float64 numpy LayerNorm (biased variance), the checker of adaln
 
 Each function is pinned by tests/test_oracle.py (closed forms, invariants,
 library routines and float64 brute force); see that file's header.
@@ -321,3 +324,54 @@ def unpatchify(y, grid, patch_size, c):
     p, q, r = patch_size
     B = y.shape[0]
     return y.view(B, f, h, w, p, q, r, c).permute(0, 7, 1, 4, 2, 5, 3, 6).reshape(B, c, f * p, h * q, w * r)
+
+
+def adaln(x: torch.Tensor, y: Optional[torch.Tensor] = None, e: Optional[torch.Tensor] = None,
+          frames: int = 1, gate_idx: int = -1, shift_idx: int = -1, scale_idx: int = -1,
+          ln_weight: Optional[torch.Tensor] = None, ln_bias: Optional[torch.Tensor] = None,
+          eps: float = EPS, norm: bool = True):
+    """One adaLN stage of a WanAttentionBlock with the reference's bf16 rounding points,
+    as torch CPU ops in the order the reference's eager graph runs them:
+
+      x + _gate(y, e[gate])          models/fast_dit.py:294,311 (_gate :179-181), or x + y (:306)
+      WanLayerNorm(r)                wan/modules/model.py:89-99: F.layer_norm on bf16 input
+      _modulate(ln, e[shift], e[scale])   models/fast_dit.py:172-177, :280,307
+
+    x, y [B, L, C]; e [frames, 6, C] (block modulation + per-frame time projection).
+    Returns (r, h) with h None when norm is False."""
+    x = x.bfloat16()
+    B, L, C = x.shape
+
+    def rows(i):
+        return e[:, i].bfloat16().unsqueeze(0)          # [1, F, C]
+
+    def per_frame(t):
+        return t.view(B, frames, L // frames, C)
+
+    r = x
+    if y is not None:
+        y = y.bfloat16()
+        if gate_idx >= 0:
+            y = (per_frame(y) * rows(gate_idx).unsqueeze(2)).view(B, L, C)
+        r = x + y
+    if not norm:
+        return r, None
+    w = None if ln_weight is None else ln_weight.bfloat16()
+    b = None if ln_bias is None else ln_bias.bfloat16()
+    h = F.layer_norm(r, (C,), w, b, eps)
+    if shift_idx >= 0:
+        h = (per_frame(h) * (1 + rows(scale_idx).unsqueeze(2)) + rows(shift_idx).unsqueeze(2)).view(B, L, C)
+    return r, h
+
+
+def layer_norm64(x: np.ndarray, w: Optional[np.ndarray] = None, b: Optional[np.ndarray] = None,
+                 eps: float = EPS) -> np.ndarray:
+    """LayerNorm over the last axis in float64: (x - mean) / sqrt(var + eps) [* w + b], with
+    the biased variance torch.nn.LayerNorm uses."""
+    x = np.asarray(x, dtype=np.float64)
+    mu = x.mean(-1, keepdims=True)
+    var = ((x - mu) ** 2).mean(-1, keepdims=True)
+    out = (x - mu) / np.sqrt(var + eps)
+    if w is not None:
+        out = out * np.asarray(w, dtype=np.float64) + np.asarray(b, dtype=np.float64)
+    return out

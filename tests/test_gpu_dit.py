@@ -1,10 +1,15 @@
-"""GPU: the block and DiT forward with the HIP attention backend (FAST_ATTN_IMPL="hip").
+"""GPU: the block and DiT forward with the HIP attention backend (FAST_ATTN_IMPL="hip")
+and the fused pointwise chain (FAST_POINTWISE_IMPL="hip").
 
   * tiny DiT (head_dim 128, 2 layers): the CFG noise prediction against the fp32 CPU
-    oracle (oracle.dit_forward), and against the same code with the torch-SDPA backend;
+    oracle (oracle.dit_forward), and against the reference-shaped path (torch SDPA and the
+    eager pointwise ops);
   * one full-width WanAttentionBlock (dim 3072, 24 heads, ffn 14336) against the fp32 CPU
     oracle (oracle.block_forward) at a short sequence, and at the full L=7854 (config D)
-    against the torch-SDPA backend on the GPU;
+    against the reference-shaped path on the GPU;
+  * the fused pointwise chain against the eager one with the same attention kernels;
+  * the patch-embedding GEMM against the Conv3d it replaces, and the FFN's GELU epilogue
+    being the tanh form of nn.GELU(approximate="tanh");
   * masked cross-attention (per-sample text lengths) through the whole block.
 Tolerances are rel-RMS: bf16 weights and activations against fp32 arithmetic.
 """
@@ -12,6 +17,7 @@ import copy
 
 import pytest
 import torch
+import torch.nn.functional as F
 
 from oracle import ref
 
@@ -39,7 +45,8 @@ def test_tiny_dit_hip_vs_oracle(W):
     ctx_c, ctx_n = torch.randn(1, 7, 64, generator=g), torch.randn(1, 7, 64, generator=g)
     outs = {}
     for impl in ("hip", "sdpa"):
-        fast = W.fast_dit.FastWanDiT(m, grid, 5.0, attn_impl=impl, cross_impl=impl)
+        fast = W.fast_dit.FastWanDiT(m, grid, 5.0, attn_impl=impl, cross_impl=impl,
+                                     pointwise_impl="hip" if impl == "hip" else "eager")
         fast.set_context(ctx_c.to(DEV), ctx_n.to(DEV))
         outs[impl] = fast(latent.to(DEV), torch.tensor(700)).float().cpu()
     m32 = copy.deepcopy(m).float().cpu()
@@ -89,9 +96,54 @@ def test_config_d_block_hip_vs_sdpa(W, lens):
     sk = None if lens is None else torch.tensor(lens, dtype=torch.int32, device=DEV)
     outs = {}
     for impl in ("hip", "sdpa"):
-        fb = W.fast_dit._FastBlock(blk, grid[0], impl, impl)
+        fb = W.fast_dit._FastBlock(blk, grid[0], impl, impl, "hip" if impl == "hip" else "eager")
         ck, cv = W.fast_dit._FastCrossKV(blk, impl)(ctx.to(DEV))
         outs[impl] = fb(x.to(DEV), e0.to(DEV), cos, sin, ck, cv, sk).float()
     e = ref.rel_rms(outs["hip"].cpu(), outs["sdpa"].cpu())
     print(f"config D block lens={lens}: rel_rms hip vs sdpa {e:.3e}")
     assert torch.isfinite(outs["hip"]).all() and e < 1e-2
+
+
+@pytest.mark.parametrize("grid", [(3, 6, 8), (21, 17, 22)])
+def test_fused_pointwise_matches_eager(W, grid):
+    """The same block with the four fused adaLN passes and the GELU epilogue vs the eager ops:
+    the only differences are bf16 rounding (LayerNorm sum order, GELU before the rounding)."""
+    m = _full_block(W, seed=5)
+    blk = m.blocks[0]
+    x, e0, ctx = _block_inputs(3072, grid, 512, 6)
+    e0[:, 1:] = e0[:, 1:2]
+    cos, sin = W.rope.rope_tables(m.freqs, grid, 128, DEV)
+    ck, cv = W.fast_dit._FastCrossKV(blk, "hip")(ctx.to(DEV))
+    outs = {pw: W.fast_dit._FastBlock(blk, grid[0], "hip", "hip", pw)(x.to(DEV), e0.to(DEV), cos, sin, ck, cv).float()
+            for pw in ("hip", "eager")}
+    e = ref.rel_rms(outs["hip"].cpu(), outs["eager"].cpu())
+    print(f"grid {grid}: fused vs eager pointwise rel_rms {e:.3e}")
+    assert torch.isfinite(outs["hip"]).all() and e < 5e-3
+
+
+def test_patch_gemm_matches_conv3d(W):
+    cfg = W.model.WanConfig(**TINY)
+    m = W.model.random_model(cfg, device=DEV, std=0.05, seed=1)
+    fast = W.fast_dit.FastWanDiT(m, (3, 4, 5), 5.0)
+    g = torch.Generator().manual_seed(3)
+    latent = torch.randn(4, 3, 8, 10, generator=g)
+    got = fast.patch(latent.to(DEV)).float().cpu()
+    conv = m.patch_embedding
+    want = F.conv3d(latent.bfloat16().float().unsqueeze(0), conv.weight.float().cpu(), conv.bias.float().cpu(),
+                    stride=conv.stride).flatten(2).transpose(1, 2)
+    assert got.shape == (2, 60, cfg.dim)
+    assert torch.equal(got[0], got[1])
+    assert ref.rel_rms(got[:1], want) < 5e-3
+
+
+def test_ffn_gelu_epilogue_is_tanh_form(W):
+    """torch._addmm_activation(use_gelu=True) (the FFN-up GEMM of the fused block) applies
+    the tanh-approximate GELU of nn.GELU(approximate="tanh") (wan/modules/model.py FFN).
+    Checked in fp32, where tanh and erf GELU differ by far more than the GEMM's rounding."""
+    xs = torch.linspace(-5, 5, 2048, device=DEV).view(2, 1024)
+    eye = torch.eye(1024, device=DEV)
+    y = torch._addmm_activation(torch.zeros(1024, device=DEV), xs, eye, use_gelu=True)
+    d_tanh = float((y - F.gelu(xs, approximate="tanh")).abs().max())
+    d_erf = float((y - F.gelu(xs)).abs().max())
+    print(f"gelu epilogue: max diff vs tanh {d_tanh:.2e}, vs erf {d_erf:.2e}")
+    assert d_tanh < 1e-5 < d_erf

@@ -111,3 +111,37 @@ def test_custom_ops_have_fake_kernels(W):
     assert out.shape == q.shape and out.device.type == "meta"
     out = torch.ops.wan_hip.cross_attn(q, q[:, :7], q[:, :7], None, 0.1)
     assert out.shape == q.shape
+
+
+def test_adaln_validation_without_launching(W):
+    N = W._native
+    lib = N.lib()
+    P = 256  # an aligned non-NULL stand-in pointer: every call below fails before any launch
+    # dim not a multiple of 8 / too large
+    assert lib.wan_adaln(P, None, None, P, 1, 4, 12, None, 1, -1, -1, -1, None, None, 1e-6, None) == 2
+    assert lib.wan_adaln(P, None, None, P, 1, 4, 8200, None, 1, -1, -1, -1, None, None, 1e-6, None) == 2
+    # seqlen not a multiple of frames
+    rc = lib.wan_adaln(P, None, None, P, 1, 10, 64, P, 3, -1, 0, 1, None, None, 1e-6, None)
+    assert rc == 1 and "frames" in N.last_error()
+    # shift without scale, row index out of range
+    assert lib.wan_adaln(P, None, None, P, 1, 4, 64, P, 1, -1, 0, -1, None, None, 1e-6, None) == 1
+    assert lib.wan_adaln(P, P, P, P, 1, 4, 64, P, 1, 6, -1, -1, None, None, 1e-6, None) == 1
+    # gate without y; modulation rows without e; weight without bias; misaligned
+    assert lib.wan_adaln(P, None, None, P, 1, 4, 64, P, 1, 2, -1, -1, None, None, 1e-6, None) == 1
+    assert lib.wan_adaln(P, None, None, P, 1, 4, 64, None, 1, -1, 0, 1, None, None, 1e-6, None) == 1
+    assert lib.wan_adaln(P, None, None, P, 1, 4, 64, None, 1, -1, -1, -1, P, None, 1e-6, None) == 1
+    rc = lib.wan_adaln(P + 2, None, None, P, 1, 4, 64, None, 1, -1, -1, -1, None, None, 1e-6, None)
+    assert rc == 1 and "aligned" in N.last_error()
+    # modulation without an output row
+    assert lib.wan_adaln(P, P, P, None, 1, 4, 64, P, 1, -1, 0, 1, None, None, 1e-6, None) == 1
+    # nothing to do is not an error
+    assert lib.wan_adaln(P, None, None, P, 0, 4, 64, None, 1, -1, -1, -1, None, None, 1e-6, None) == 0
+
+
+def test_adaln_op_validates_on_cpu(W):
+    x = torch.zeros(1, 4, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="CUDA"):
+        W.ops.adaln(x)
+    xm = torch.empty(2, 12, 64, dtype=torch.bfloat16, device="meta")
+    r, h = torch.ops.wan_hip.adaln(xm, xm, None, 3, -1, -1, -1, None, None, 1e-6, True)
+    assert r.shape == xm.shape and h.shape == xm.shape

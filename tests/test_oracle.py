@@ -326,3 +326,117 @@ def test_planted_rms_mistakes_are_caught(golden):
     assert ref.rel_rms(path(ref.rms), want) < 1e-5
     assert ref.rel_rms(path(per_head), want) > 1e-3
     assert ref.rel_rms(path(no_gamma), want) > 1e-3
+
+
+# ---------------------------------------------------------------------------
+# adaLN stage (ref.adaln): LayerNorm against float64, closed forms of the
+# modulation / gate, the per-frame row mapping, and planted mistakes
+# ---------------------------------------------------------------------------
+
+def _bf16_ulp_close(got: torch.Tensor, want64: np.ndarray, ulps: float = 1.0) -> bool:
+    """|got - want| within `ulps` bf16 ulps of |want| (absolute floor 2^-30)."""
+    g = got.double().numpy()
+    w = np.asarray(want64, dtype=np.float64)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(w), 2.0 ** -30))) - 7)
+    return bool((np.abs(g - w) <= ulps * ulp).all())
+
+
+def check_adaln_layer_norm(fn) -> bool:
+    x = (_r((2, 6, 256), 40) * 3 + 1).bfloat16()
+    w, b = (1 + 0.3 * _r((256,), 41)).bfloat16(), (0.2 * _r((256,), 42)).bfloat16()
+    _, h = fn(x, ln_weight=w, ln_bias=b)
+    want = ref.layer_norm64(x.double().numpy(), w.double().numpy(), b.double().numpy(), ref.EPS)
+    _, h0 = fn(x)
+    want0 = ref.layer_norm64(x.double().numpy(), eps=ref.EPS)
+    return _bf16_ulp_close(h, want) and _bf16_ulp_close(h0, want0)
+
+
+def check_adaln_frames_and_gate(fn) -> bool:
+    """Frame f's tokens take row f of e: with scale = -1 the modulation returns the shift row
+    exactly; a zero gate leaves x, a unit gate gives bf16(x + y), no gate adds y."""
+    B, Fr, per, C = 2, 3, 5, 64
+    x, y = _r((B, Fr * per, C), 43).bfloat16(), _r((B, Fr * per, C), 44).bfloat16()
+    e = torch.zeros(Fr, 6, C)
+    e[:, 1] = -1.0                                       # scale row: 1 + scale = 0
+    e[:, 0] = torch.arange(Fr, dtype=torch.float32).view(Fr, 1) + 0.5 * torch.arange(C) / C
+    e[:, 2] = torch.tensor([0.0, 1.0, 0.0]).view(Fr, 1)  # gate row: 0 / 1 / 0 by frame
+    e = e.bfloat16()
+    _, h = fn(x, e=e, frames=Fr, shift_idx=0, scale_idx=1)
+    want_h = e[:, 0].unsqueeze(1).expand(Fr, per, C).reshape(1, Fr * per, C).expand(B, -1, -1)
+    r, _ = fn(x, y, e=e, frames=Fr, gate_idx=2, norm=False)
+    gmask = torch.tensor([0.0, 1.0, 0.0]).repeat_interleave(per).view(1, -1, 1).bool()
+    want_r = torch.where(gmask, (x.float() + y.float()).bfloat16(), x)
+    r2, _ = fn(x, y, norm=False)
+    return (torch.equal(h, want_h) and torch.equal(r, want_r)
+            and torch.equal(r2, (x.float() + y.float()).bfloat16()))
+
+
+def check_adaln_zero_modulation(fn) -> bool:
+    x = _r((1, 8, 128), 45).bfloat16()
+    e = torch.zeros(2, 6, 128).bfloat16()
+    _, h = fn(x, e=e, frames=2, shift_idx=3, scale_idx=4)
+    _, ln = fn(x)
+    return torch.equal(h, ln)
+
+
+def test_adaln_layer_norm_matches_float64():
+    assert check_adaln_layer_norm(ref.adaln)
+
+
+def test_adaln_layer_norm_known_answer():
+    x = torch.tensor([[[1.0, 2.0, 3.0, 4.0]]]).bfloat16()
+    _, h = ref.adaln(x, eps=0.0)
+    want = (np.array([1, 2, 3, 4]) - 2.5) / math.sqrt(1.25)
+    assert _bf16_ulp_close(h[0, 0], want)
+
+
+def test_adaln_frames_gate_and_zero_modulation():
+    assert check_adaln_frames_and_gate(ref.adaln)
+    assert check_adaln_zero_modulation(ref.adaln)
+
+
+def _adaln_unbiased_var(x, y=None, e=None, frames=1, gate_idx=-1, shift_idx=-1, scale_idx=-1,
+                        ln_weight=None, ln_bias=None, eps=ref.EPS, norm=True):
+    r, _ = ref.adaln(x, y, e, frames, gate_idx, norm=False)
+    if not norm:
+        return r, None
+    n = r.shape[-1]
+    rf = r.float()
+    h = ((rf - rf.mean(-1, keepdim=True)) / torch.sqrt(rf.var(-1, keepdim=True) + eps))
+    if ln_weight is not None:
+        h = h * ln_weight.float() + ln_bias.float()
+    h = h.bfloat16()
+    assert n > 1
+    if shift_idx >= 0:
+        B, L, C = h.shape
+        h = (h.view(B, frames, L // frames, C) * (1 + e[:, scale_idx].unsqueeze(0).unsqueeze(2))
+             + e[:, shift_idx].unsqueeze(0).unsqueeze(2)).view(B, L, C)
+    return r, h
+
+
+def _adaln_frames_interleaved(x, y=None, e=None, frames=1, gate_idx=-1, shift_idx=-1, scale_idx=-1,
+                              ln_weight=None, ln_bias=None, eps=ref.EPS, norm=True):
+    # token l taken as frame l % frames instead of l // (L / frames)
+    B, L, C = x.shape
+    perm = torch.arange(L).view(L // frames, frames).t().reshape(-1)
+    inv = torch.argsort(perm)
+    r, h = ref.adaln(x[:, perm], None if y is None else y[:, perm], e, frames, gate_idx, shift_idx,
+                     scale_idx, ln_weight, ln_bias, eps, norm)
+    return r[:, inv], None if h is None else h[:, inv]
+
+
+def _adaln_gate_on_x(x, y=None, e=None, frames=1, gate_idx=-1, shift_idx=-1, scale_idx=-1,
+                     ln_weight=None, ln_bias=None, eps=ref.EPS, norm=True):
+    # the gate multiplies the residual instead of the branch output
+    if y is not None and gate_idx >= 0:
+        B, L, C = x.shape
+        xg = (x.view(B, frames, L // frames, C) * e[:, gate_idx].unsqueeze(0).unsqueeze(2)).view(B, L, C)
+        return ref.adaln(xg, y, None, frames, -1, shift_idx, scale_idx, ln_weight, ln_bias, eps, norm)
+    return ref.adaln(x, y, e, frames, gate_idx, shift_idx, scale_idx, ln_weight, ln_bias, eps, norm)
+
+
+@pytest.mark.parametrize("mutant", [_adaln_unbiased_var, _adaln_frames_interleaved, _adaln_gate_on_x])
+def test_planted_adaln_mistakes_are_caught(mutant):
+    ok = (check_adaln_layer_norm(mutant) and check_adaln_frames_and_gate(mutant)
+          and check_adaln_zero_modulation(mutant))
+    assert not ok

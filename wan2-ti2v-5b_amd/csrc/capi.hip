@@ -303,4 +303,50 @@ int wan_rope(wan_tensor x, void* out, int batch, int seqlen, int heads, int head
   return launch_rope(a, static_cast<hipStream_t>(stream));
 }
 
+int wan_adaln(const void* x, const void* y, void* x_out, void* h_out, int batch, int seqlen,
+              int dim, const void* e, int frames, int gate_idx, int shift_idx, int scale_idx,
+              const void* ln_weight, const void* ln_bias, float eps, void* stream) {
+  const char* fn = "wan_adaln";
+  if (batch < 0 || seqlen < 0 || dim <= 0 || frames <= 0)
+    return set_error(WAN_ERR_INVALID, "%s: bad sizes (batch=%d seqlen=%d dim=%d frames=%d)", fn,
+                     batch, seqlen, dim, frames);
+  if (dim % 8 != 0 || dim > 8192)
+    return set_error(WAN_ERR_UNSUPPORTED, "%s: dim=%d must be a multiple of 8 and <= 8192", fn, dim);
+  if (seqlen % frames != 0)
+    return set_error(WAN_ERR_INVALID, "%s: seqlen=%d is not a multiple of frames=%d", fn, seqlen,
+                     frames);
+  if (gate_idx < -1 || gate_idx > 5 || shift_idx < -1 || shift_idx > 5 || scale_idx < -1 ||
+      scale_idx > 5 || ((shift_idx < 0) != (scale_idx < 0)))
+    return set_error(WAN_ERR_INVALID, "%s: modulation rows gate=%d shift=%d scale=%d out of range",
+                     fn, gate_idx, shift_idx, scale_idx);
+  if (x == nullptr || (y == nullptr && x_out != nullptr) || (gate_idx >= 0 && y == nullptr))
+    return set_error(WAN_ERR_INVALID, "%s: x is NULL, or x_out / a gate given without y", fn);
+  if (h_out == nullptr && (shift_idx >= 0 || ln_weight != nullptr))
+    return set_error(WAN_ERR_INVALID, "%s: modulation or LayerNorm weights given without h_out", fn);
+  if ((gate_idx >= 0 || shift_idx >= 0) && e == nullptr)
+    return set_error(WAN_ERR_INVALID, "%s: modulation rows requested but e is NULL", fn);
+  if ((ln_weight == nullptr) != (ln_bias == nullptr))
+    return set_error(WAN_ERR_INVALID, "%s: LayerNorm weight and bias must be given together", fn);
+  const void* ptrs[] = {x, y, x_out, h_out, e, ln_weight, ln_bias};
+  for (const void* p : ptrs)
+    if (!aligned16(p)) return set_error(WAN_ERR_INVALID, "%s: operands must be 16-byte aligned", fn);
+  AdaLNArgs a;
+  a.x = static_cast<const bf16*>(x);
+  a.y = static_cast<const bf16*>(y);
+  a.x_out = static_cast<bf16*>(x_out);
+  a.h_out = static_cast<bf16*>(h_out);
+  a.B = batch;
+  a.L = seqlen;
+  a.C = dim;
+  a.F = frames;
+  a.e = static_cast<const bf16*>(e);
+  a.gate_idx = gate_idx;
+  a.shift_idx = shift_idx;
+  a.scale_idx = scale_idx;
+  a.ln_w = static_cast<const bf16*>(ln_weight);
+  a.ln_b = static_cast<const bf16*>(ln_bias);
+  a.eps = eps;
+  return launch_adaln(a, static_cast<hipStream_t>(stream));
+}
+
 }  // extern "C"

@@ -74,6 +74,23 @@ struct RopeArgs {
 };
 int launch_rope(const RopeArgs& a, hipStream_t s);
 
+// One adaLN stage of a block: residual update, LayerNorm, per-frame modulation.
+struct AdaLNArgs {
+  const bf16* x;        // [B, L, C] residual stream
+  const bf16* y;        // [B, L, C] branch output added to x (null: none)
+  bf16* x_out;          // [B, L, C] updated residual (null: not written)
+  bf16* h_out;          // [B, L, C] normalised (and modulated) row (null: no LayerNorm)
+  int B, L, C, F;       // F frames of L / F contiguous tokens each
+  const bf16* e;        // [F, 6, C] modulation rows (block modulation + time projection)
+  int gate_idx;         // row of e gating y (-1: ungated)
+  int shift_idx;        // rows of e for the modulation (-1: none)
+  int scale_idx;
+  const bf16* ln_w;     // [C] LayerNorm affine weight / bias (null: not affine)
+  const bf16* ln_b;
+  float eps;
+};
+int launch_adaln(const AdaLNArgs& a, hipStream_t s);
+
 enum QPrep { kQPlain = 0, kQNorm = 1, kQNormRope = 2 };
 
 struct FlashArgs {

@@ -11,6 +11,10 @@ batch 2, on one GPU:
                      "sdpa" torch's F.scaled_dot_product_attention after separate
                             QK-RMSNorm / RoPE ops (_sdpa, models/fast_dit.py:186-189)
   FAST_CROSS_IMPL  cross-attention backend, defaults to FAST_ATTN_IMPL (:45, :299-304)
+  FAST_POINTWISE_IMPL  the block's pointwise chain (LayerNorms, _modulate, _gate, residual adds):
+                     "hip"  (default) one fused pass per stage (ops.adaln) and the FFN's
+                            tanh-GELU as the epilogue of its first GEMM
+                     "eager" the separate torch ops of models/fast_dit.py:280-311
 
   _tp_rms_qk, _tp_rms  models/fast_dit.py:134-160 (TP=1: the all-reduce is the identity)
   _rope                models/fast_dit.py:163-169
@@ -23,8 +27,9 @@ Differences from the reference, all on purpose: no torch.compile (the
 reference compiles each block for Neuron; here the hot ops are hand-written
 kernels and the rest is eager PyTorch / hipBLASLt), the q/k/v projections of
 the "hip" path run as one GEMM on concatenated weights (the kernels read q, k, v
-as strided views of its output), and cross-attention takes optional per-sample
-text lengths.
+as strided views of its output), cross-attention takes optional per-sample
+text lengths, and the patch embedding (a Conv3d whose stride equals its
+kernel) runs as the equivalent GEMM over gathered patches.
 """
 import os
 from typing import Optional, Sequence
@@ -38,10 +43,13 @@ from .model import WanModel, sinusoidal_embedding_1d
 
 FAST_ATTN_IMPL = os.environ.get("FAST_ATTN_IMPL", "hip")
 FAST_CROSS_IMPL = os.environ.get("FAST_CROSS_IMPL", FAST_ATTN_IMPL)
+FAST_POINTWISE_IMPL = os.environ.get("FAST_POINTWISE_IMPL", "hip")
 IMPLS = ("hip", "sdpa")
 for _name, _val in (("FAST_ATTN_IMPL", FAST_ATTN_IMPL), ("FAST_CROSS_IMPL", FAST_CROSS_IMPL)):
     if _val not in IMPLS:
         raise ValueError(f"{_name}={_val!r}: expected one of {IMPLS}")
+if FAST_POINTWISE_IMPL not in ("hip", "eager"):
+    raise ValueError(f"FAST_POINTWISE_IMPL={FAST_POINTWISE_IMPL!r}: expected 'hip' or 'eager'")
 
 
 def _lin(x, layer):
@@ -124,11 +132,12 @@ class _FastBlock:
     """One WanAttentionBlock forward (models/fast_dit.py:260-311) at TP=1."""
 
     def __init__(self, block, num_frames: int, attn_impl: str = FAST_ATTN_IMPL,
-                 cross_impl: str = FAST_CROSS_IMPL):
+                 cross_impl: str = FAST_CROSS_IMPL, pointwise_impl: str = FAST_POINTWISE_IMPL):
         self.block = block
         self.num_frames = num_frames
         self.attn_impl = attn_impl
         self.cross_impl = cross_impl
+        self.pointwise_impl = pointwise_impl
         sa = block.self_attn
         if attn_impl == "hip":
             self.w_qkv = torch.cat([sa.q.weight, sa.k.weight, sa.v.weight], 0).contiguous()
@@ -138,43 +147,67 @@ class _FastBlock:
         blk, nf = self.block, self.num_frames
         sa, ca = blk.self_attn, blk.cross_attn
         B, L, C = x.shape
-        n, d = sa.num_heads, sa.head_dim
 
+        if self.pointwise_impl == "hip" and x.is_cuda:
+            return self._fused(x, e0, cos, sin, ck, cv, seqlen_k)
         e = (blk.modulation.unsqueeze(0) + e0).chunk(6, dim=2)
         e = [t.squeeze(2) for t in e]  # each [1, F, C]
 
         # self-attention
         h = _modulate(blk.norm1(x).to(torch.bfloat16), e[0], e[1], nf)
-        if self.attn_impl == "hip":
-            qkv = F.linear(h, self.w_qkv, self.b_qkv)  # [B, L, 3C]
-            q = qkv[..., :C].view(B, L, n, d)
-            k = qkv[..., C:2 * C].view(B, L, n, d)
-            v = qkv[..., 2 * C:].view(B, L, n, d)
-            y = _hip_self_fused(q, k, v, sa.norm_q, sa.norm_k, cos, sin)
-        else:
-            q, k = _tp_rms_qk(_lin(h, sa.q), _lin(h, sa.k), sa.norm_q, sa.norm_k)
-            v = _lin(h, sa.v).view(B, L, n, d)
-            q = _rope(q.view(B, L, n, d), cos, sin)
-            k = _rope(k.view(B, L, n, d), cos, sin)
-            y = _sdpa(q, k, v)
-        y = _lin(y.reshape(B, L, C), sa.o)
+        y = _lin(self._self_attn(h, cos, sin).reshape(B, L, C), sa.o)
         x = x + _gate(y, e[2], nf)
 
         # cross-attention; ck/cv [B, Lc, n, d] precomputed once per prompt (_FastCrossKV)
         h = blk.norm3(x)
-        if self.cross_impl == "hip":
-            q = _lin(h, ca.q).view(B, L, n, d)
-            y = _hip_cross_fused(q, ck, cv, ca.norm_q, seqlen_k)
-        else:
-            q = _tp_rms(_lin(h, ca.q), ca.norm_q).view(B, L, n, d)
-            y = _sdpa(q, ck, cv, None if seqlen_k is None else seqlen_k.tolist())
-        x = x + _lin(y.reshape(B, L, C), ca.o)
+        x = x + _lin(self._cross_attn(h, ck, cv, seqlen_k).reshape(B, L, C), ca.o)
 
         # FFN
         h = _modulate(blk.norm2(x).to(torch.bfloat16), e[3], e[4], nf)
         h = blk.ffn[1](_lin(h, blk.ffn[0]))
         y = _lin(h, blk.ffn[2])
         return x + _gate(y, e[5], nf)
+
+    def _self_attn(self, h, cos, sin):
+        blk = self.block
+        sa = blk.self_attn
+        B, L, C = h.shape
+        n, d = sa.num_heads, sa.head_dim
+        if self.attn_impl == "hip":
+            qkv = F.linear(h, self.w_qkv, self.b_qkv)
+            q, k, v = (qkv[..., i * C:(i + 1) * C].view(B, L, n, d) for i in range(3))
+            return _hip_self_fused(q, k, v, sa.norm_q, sa.norm_k, cos, sin)
+        q, k = _tp_rms_qk(_lin(h, sa.q), _lin(h, sa.k), sa.norm_q, sa.norm_k)
+        v = _lin(h, sa.v).view(B, L, n, d)
+        return _sdpa(_rope(q.view(B, L, n, d), cos, sin), _rope(k.view(B, L, n, d), cos, sin), v)
+
+    def _cross_attn(self, h, ck, cv, seqlen_k):
+        ca = self.block.cross_attn
+        B, L, C = h.shape
+        n, d = ca.num_heads, ca.head_dim
+        if self.cross_impl == "hip":
+            return _hip_cross_fused(_lin(h, ca.q).view(B, L, n, d), ck, cv, ca.norm_q, seqlen_k)
+        q = _tp_rms(_lin(h, ca.q), ca.norm_q).view(B, L, n, d)
+        return _sdpa(q, ck, cv, None if seqlen_k is None else seqlen_k.tolist())
+
+    def _fused(self, x, e0, cos, sin, ck, cv, seqlen_k):
+        """The same block with its pointwise chain in four fused adaLN passes
+        (models/fast_dit.py:280, :294, :306-307, :311) and GELU in the FFN-up GEMM."""
+        blk, nf = self.block, self.num_frames
+        B, L, C = x.shape
+        e = (blk.modulation.unsqueeze(0) + e0).reshape(nf, 6, C)      # rows 0..5 per frame
+        x = x.contiguous()
+        _, h = ops.adaln(x, e=e, frames=nf, shift_idx=0, scale_idx=1, eps=blk.norm1.eps)
+        y = _lin(self._self_attn(h, cos, sin).reshape(B, L, C), blk.self_attn.o)
+        x, h = ops.adaln(x, y, e, nf, gate_idx=2, ln_weight=blk.norm3.weight,
+                         ln_bias=blk.norm3.bias, eps=blk.norm3.eps)
+        y = _lin(self._cross_attn(h, ck, cv, seqlen_k).reshape(B, L, C), blk.cross_attn.o)
+        x, h = ops.adaln(x, y, e, nf, shift_idx=3, scale_idx=4, eps=blk.norm2.eps)
+        f0, f2 = blk.ffn[0], blk.ffn[2]
+        h = torch._addmm_activation(f0.bias, h.view(B * L, C), f0.weight.t(), use_gelu=True)
+        y = _lin(h.view(B, L, -1), f2)
+        x, _ = ops.adaln(x, y, e, nf, gate_idx=5, norm=False)
+        return x
 
 
 class _FastCrossKV:
@@ -230,7 +263,7 @@ class FastWanDiT:
     """
 
     def __init__(self, model: WanModel, grid, guide_scale: float, attn_impl: str = FAST_ATTN_IMPL,
-                 cross_impl: str = FAST_CROSS_IMPL):
+                 cross_impl: str = FAST_CROSS_IMPL, pointwise_impl: str = FAST_POINTWISE_IMPL):
         self.model = model
         self.grid = tuple(int(g) for g in grid)
         self.num_frames = self.grid[0]
@@ -239,7 +272,8 @@ class FastWanDiT:
         self.device = dev
         head_dim = model.dim // model.num_heads
         self.cos, self.sin = _rope_mod.rope_tables(model.freqs, self.grid, head_dim, dev)
-        self.blocks = [_FastBlock(b, self.num_frames, attn_impl, cross_impl) for b in model.blocks]
+        self.blocks = [_FastBlock(b, self.num_frames, attn_impl, cross_impl, pointwise_impl)
+                       for b in model.blocks]
         self.cross_kv = [_FastCrossKV(b, cross_impl) for b in model.blocks]
         self.head = _FastHead(model.head, self.grid, model.patch_size, model.out_dim, guide_scale)
         self.context = None
@@ -266,9 +300,16 @@ class FastWanDiT:
         return e, e0
 
     def patch(self, latent):
-        x = self.model.patch_embedding(latent.unsqueeze(0).to(torch.bfloat16))  # [1, C, f, h, w]
-        x = x.flatten(2).transpose(1, 2)                                         # [1, L, C]
-        return x.expand(2, -1, -1).contiguous()
+        """Patch embedding (a Conv3d with stride = kernel = patch_size) as one GEMM: gather
+        each patch's in_dim x pt x ph x pw values in the weight's (c, t, h, w) order, then
+        [L, in_dim*pt*ph*pw] x [dim, in_dim*pt*ph*pw]^T + bias.  Token order f, y, x."""
+        conv = self.model.patch_embedding
+        c, f, H, W = latent.shape
+        pt, ph, pw = conv.kernel_size
+        p = latent.to(torch.bfloat16).view(c, f // pt, pt, H // ph, ph, W // pw, pw)
+        p = p.permute(1, 3, 5, 0, 2, 4, 6).reshape((f // pt) * (H // ph) * (W // pw), c * pt * ph * pw)
+        x = F.linear(p, conv.weight.view(conv.weight.shape[0], -1), conv.bias)   # [L, C]
+        return x.unsqueeze(0).expand(2, -1, -1).contiguous()
 
     def __call__(self, latent, t):
         assert self.context is not None, "call set_context() first"

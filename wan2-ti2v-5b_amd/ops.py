@@ -8,7 +8,7 @@ from torch's caching allocator; the native side allocates nothing.
 
 The fake (meta) kernels let torch.compile trace the ops without running them.
 """
-from typing import Optional
+from typing import Optional, Tuple
 
 import torch
 
@@ -279,3 +279,71 @@ def flash_attn_qnorm(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, inv_rms_
 @flash_attn_qnorm.register_fake
 def _(q, k, v, inv_rms_q, gamma_q, cos, sin, seqlen_k, softmax_scale):
     return q.new_empty(q.shape)
+
+
+# ─── adaLN: the pointwise stages of a WanAttentionBlock ─────────────────────
+
+def _check_rows(fn: str, name: str, t: torch.Tensor, shape, device) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{fn}: {name} must be a tensor, got {type(t).__name__}")
+    if t.dtype != torch.bfloat16 or t.device != device or tuple(t.shape) != tuple(shape) \
+            or not t.is_contiguous() or (t.numel() and t.data_ptr() % 16):
+        raise ValueError(f"{fn}: {name} must be a contiguous, 16-byte aligned bf16 tensor of shape "
+                         f"{tuple(shape)} on {device}, got {t.dtype} {tuple(t.shape)} on {t.device}")
+
+
+@torch.library.custom_op("wan_hip::adaln", mutates_args=())
+def adaln_stage(x: torch.Tensor, y: Optional[torch.Tensor], e: Optional[torch.Tensor], frames: int,
+                gate_idx: int, shift_idx: int, scale_idx: int, ln_weight: Optional[torch.Tensor],
+                ln_bias: Optional[torch.Tensor], eps: float, norm: bool) -> Tuple[torch.Tensor, torch.Tensor]:
+    """One fused adaLN stage (see adaln()).  Returns (x_out, h); x_out is empty when y is
+    None and h is empty when norm is False."""
+    fn = "adaln"
+    if not isinstance(x, torch.Tensor) or x.dim() != 3:
+        raise ValueError(f"{fn}: x must be a [B, L, C] tensor")
+    B, L, C = x.shape
+    if x.device.type != "cuda":
+        raise ValueError(f"{fn}: expected a CUDA (HIP) tensor, got device {x.device}")
+    _check_rows(fn, "x", x, (B, L, C), x.device)
+    if y is not None:
+        _check_rows(fn, "y", y, (B, L, C), x.device)
+    if e is not None:
+        _check_rows(fn, "e", e, (frames, 6, C), x.device)
+    if ln_weight is not None or ln_bias is not None:
+        if ln_weight is None or ln_bias is None:
+            raise ValueError(f"{fn}: give the LayerNorm weight and bias together")
+        _check_rows(fn, "ln_weight", ln_weight, (C,), x.device)
+        _check_rows(fn, "ln_bias", ln_bias, (C,), x.device)
+    x_out = torch.empty_like(x) if y is not None else x.new_empty((0,))
+    h = torch.empty_like(x) if norm else x.new_empty((0,))
+    with torch.cuda.device(x.device):
+        N.check("wan_adaln", N.lib().wan_adaln(
+            x.data_ptr(), None if y is None else y.data_ptr(),
+            None if y is None else x_out.data_ptr(), h.data_ptr() if norm else None,
+            B, L, C, None if e is None else e.data_ptr(), int(frames), int(gate_idx),
+            int(shift_idx), int(scale_idx),
+            None if ln_weight is None else ln_weight.data_ptr(),
+            None if ln_bias is None else ln_bias.data_ptr(), float(eps), _stream(x.device)))
+    return x_out, h
+
+
+@adaln_stage.register_fake
+def _(x, y, e, frames, gate_idx, shift_idx, scale_idx, ln_weight, ln_bias, eps, norm):
+    x_out = x.new_empty(x.shape) if y is not None else x.new_empty((0,))
+    h = x.new_empty(x.shape) if norm else x.new_empty((0,))
+    return x_out, h
+
+
+def adaln(x: torch.Tensor, y: Optional[torch.Tensor] = None, e: Optional[torch.Tensor] = None,
+          frames: int = 1, gate_idx: int = -1, shift_idx: int = -1, scale_idx: int = -1,
+          ln_weight: Optional[torch.Tensor] = None, ln_bias: Optional[torch.Tensor] = None,
+          eps: float = 1e-6, norm: bool = True):
+    """The pointwise work of one WanAttentionBlock stage (models/fast_dit.py:280,294,306-311),
+    on x [B, L, C] bf16 with the block's modulation rows e [frames, 6, C]:
+
+        r = x  |  bf16(x + y)  |  bf16(x + bf16(y * e[f, gate_idx]))
+        h = bf16(LayerNorm(r) [* w + b])  [then bf16(bf16(h * bf16(1 + e[f, scale_idx])) + e[f, shift_idx])]
+
+    Returns (r, h); h is None when norm is False."""
+    r, h = adaln_stage(x, y, e, frames, gate_idx, shift_idx, scale_idx, ln_weight, ln_bias, eps, norm)
+    return (x if y is None else r), (h if norm else None)
