@@ -38,7 +38,9 @@
 //    inverse RMS) and the 3D-RoPE rotation are applied there, with the
 //    reference's bf16 rounding points (models/fast_dit.py:145-146,169).
 //  * Workgroup ids are remapped so each XCD owns contiguous query blocks of the
-//    same heads (K/V reuse in that XCD's L2).
+//    same heads (K/V reuse in that XCD's L2); with per-sample key lengths the
+//    batch index varies fastest instead, balancing long and short samples
+//    over the XCDs.
 #include "common.h"
 
 
@@ -204,9 +206,22 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
 
   const int num_m = (a.Lq + BM - 1) / BM;
   const int pid = xcd_remap(blockIdx.x, gridDim.x);
-  const int mblk = pid % num_m;
-  const int bh = pid / num_m;
-  const int b = bh / a.H, h = bh - b * a.H;
+  int mblk, b, h;
+  if (a.seqlen_k == nullptr) {
+    // (b, h) major: the query blocks of one head run together on one XCD and
+    // share its K/V through that XCD's L2
+    mblk = pid % num_m;
+    const int bh = pid / num_m;
+    b = bh / a.H;
+    h = bh - b * a.H;
+  } else {
+    // per-sample key lengths: batch fastest, so every XCD receives the same
+    // mix of long and short samples (the K/V of these calls are small)
+    b = pid % a.B;
+    const int rest = pid / a.B;
+    mblk = rest % num_m;
+    h = rest / num_m;
+  }
 
   int len = a.seqlen_all;
   if (a.seqlen_k != nullptr) len = min(max(a.seqlen_k[b], 0), a.Lk);

@@ -34,7 +34,9 @@ __device__ __forceinline__ void rope8(float u[8], const float* cos_row,
 }
 
 // One wave per token row: sum of squares over all H*128 channels, then
-// optionally the normalised (and rotated) row.
+// optionally the normalised (and rotated) row.  NCH: 8-channel chunks per lane
+// (H*16 <= 64*NCH), so the row's loads are issued unconditionally together.
+template <int NCH>
 __global__ __launch_bounds__(256) void rms_prep_kernel(const PrepArgs a) {
   const int lane = threadIdx.x & 63;
   const int tok = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -43,10 +45,10 @@ __global__ __launch_bounds__(256) void rms_prep_kernel(const PrepArgs a) {
   const int nchunks = a.H * 16;
   const bf16* row = a.x.ptr + b * a.x.sb + (int64_t)l * a.x.st;
 
-  bf16x8 xv[kMaxChunksPerLane];
+  bf16x8 xv[NCH];
   float ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < kMaxChunksPerLane; ++i) {
+  for (int i = 0; i < NCH; ++i) {
     const int c = lane + 64 * i;
     if (c < nchunks) {
       const int h = c >> 4, d0 = (c & 15) * 8;
@@ -67,7 +69,7 @@ __global__ __launch_bounds__(256) void rms_prep_kernel(const PrepArgs a) {
   const float* sin_row = a.sin ? a.sin + (int64_t)l * kRopePairs : nullptr;
   bf16* orow = a.out + (int64_t)tok * a.H * kHeadDim;
 #pragma unroll
-  for (int i = 0; i < kMaxChunksPerLane; ++i) {
+  for (int i = 0; i < NCH; ++i) {
     const int c = lane + 64 * i;
     if (c < nchunks) {
       const int h = c >> 4, d0 = (c & 15) * 8;
@@ -115,8 +117,15 @@ __global__ __launch_bounds__(256) void rope_kernel(const RopeArgs a) {
 int launch_rms_prep(const PrepArgs& a, hipStream_t s) {
   const int rows = a.B * a.L;
   if (rows == 0) return 0;
-  if (a.H * 16 > 64 * kMaxChunksPerLane) return set_error(2, "rms_prep: H*128=%d channels exceeds 8192", a.H * 128);
-  hipLaunchKernelGGL(rms_prep_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, a);
+  const int nch = a.H * 16;
+  if (nch > 64 * kMaxChunksPerLane) return set_error(2, "rms_prep: H*128=%d channels exceeds 8192", a.H * 128);
+  const dim3 grid((rows + 3) / 4), block(256);
+  if (nch <= 64) hipLaunchKernelGGL(rms_prep_kernel<1>, grid, block, 0, s, a);
+  else if (nch <= 128) hipLaunchKernelGGL(rms_prep_kernel<2>, grid, block, 0, s, a);
+  else if (nch <= 256) hipLaunchKernelGGL(rms_prep_kernel<4>, grid, block, 0, s, a);
+  else if (nch <= 384) hipLaunchKernelGGL(rms_prep_kernel<6>, grid, block, 0, s, a);
+  else if (nch <= 512) hipLaunchKernelGGL(rms_prep_kernel<8>, grid, block, 0, s, a);
+  else hipLaunchKernelGGL(rms_prep_kernel<16>, grid, block, 0, s, a);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? 0 : set_error(4, "rms_prep launch: %s", hipGetErrorString(e));
 }
