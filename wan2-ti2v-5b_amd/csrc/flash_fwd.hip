@@ -271,20 +271,22 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
 
     // P = exp2(S * scale*log2e - m_run) in bf16, and this lane's sum of P
     // (of the bf16 values the PV MFMAs use; v_dot2 against (1, 1)).
+    // Used off the hot loop only (the last tile and the rescale path): each
+    // quarter of the tile is a scheduling region of its own, which bounds the
+    // exponentials in flight (and the register pressure) at eight.
     auto exp_tile = [&](const f32x16& s0, const f32x16& s1, bf16x8 pb[4]) -> float {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        pb[r >> 3][r & 7] = (bf16)fast_exp2(fmaf(s0[r], sl2, -m_run));
-        pb[2 + (r >> 3)][r & 7] = (bf16)fast_exp2(fmaf(s1[r], sl2, -m_run));
-      }
       const bf16x2 one = {(bf16)1.0f, (bf16)1.0f};
       float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
+        const f32x16& sv = i < 2 ? s0 : s1;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pb[i][j] = (bf16)fast_exp2(fmaf(sv[8 * (i & 1) + j], sl2, -m_run));
         acc[i] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pb[i], pb[i], 0, 1), one, acc[i], false);
         acc[i] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pb[i], pb[i], 2, 3), one, acc[i], false);
         acc[i] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pb[i], pb[i], 4, 5), one, acc[i], false);
         acc[i] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pb[i], pb[i], 6, 7), one, acc[i], false);
+        __builtin_amdgcn_sched_barrier(0);
       }
       return (acc[0] + acc[1]) + (acc[2] + acc[3]);
     };
@@ -312,17 +314,14 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
       l_run += rs;
     };
 
-    // Softmax numerator of the last tile, keys >= len masked.
-    auto softmax_last = [&](f32x16& s0, f32x16& s1, int kt, bf16x8 pb[4]) {
-      if ((kt + BN) > len) {
+    // Sets the scores of keys >= len to -inf (a partial last tile starting at key kt).
+    auto mask_tile = [&](f32x16& s0, f32x16& s1, int kt) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kt + 8 * (r >> 2) + 4 * hh + (r & 3);
-          if (key >= len) s0[r] = -INFINITY;
-          if (key + 32 >= len) s1[r] = -INFINITY;
-        }
+      for (int r = 0; r < 16; ++r) {
+        const int key = kt + 8 * (r >> 2) + 4 * hh + (r & 3);
+        if (key >= len) s0[r] = -INFINITY;
+        if (key + 32 >= len) s1[r] = -INFINITY;
       }
-      finish(s0, s1, exp_tile(s0, s1, pb), pb);
     };
 
     // The MFMAs of S(next) = K Q^T, interleaved in program order with the
@@ -412,15 +411,22 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
       step(t, k_lds0, v_lds1, k_lds1, v_lds0, sa0, sa1, sb0, sb1);
       step(t + 1, k_lds1, v_lds0, k_lds0, v_lds1, sb0, sb1, sa0, sa1);
     }
-    bf16x8 pb[4];
-    if (t + 1 < ntiles) {  // tiles t (full) and t + 1 (last) remain
+    // One full tile may remain before the last; then the last tile's scores are
+    // moved into sa so that a single copy of the last-tile code follows (its
+    // V buffer is picked at run time; every load has landed by then).
+    const bf16* v_last = v_lds0;
+    if (t + 1 < ntiles) {
       step(t, k_lds0, v_lds1, k_lds1, v_lds0, sa0, sa1, sb0, sb1);
-      softmax_last(sb0, sb1, (t + 1) * BN, pb);
-      pv(pb, v_lds1);
-    } else {               // tile t is the last
-      softmax_last(sa0, sa1, t * BN, pb);
-      pv(pb, v_lds0);
+      sa0 = sb0;
+      sa1 = sb1;
+      v_last = v_lds1;
+      ++t;
     }
+    // the last tile, its keys >= len masked when it is partial
+    if (ntiles * BN > len) mask_tile(sa0, sa1, t * BN);
+    bf16x8 pb[4];
+    finish(sa0, sa1, exp_tile(sa0, sa1, pb), pb);
+    pv(pb, v_last);
   }
 
   const float l_tot = pair_sum(l_run);
