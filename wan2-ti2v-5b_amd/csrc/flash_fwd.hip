@@ -235,12 +235,16 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
   float l_run = 0.f;        // this lane's partial row sum (its 32 keys of each tile)
 
   if (ntiles > 0) {
-    bf16x8 qf[8];
-    load_q_fragment<QP>(a, b, h, qrow, hh, qf);
-
     TileLoader<NW> kl, vl;
     kl.init(a.k.ptr + b * a.k.sb + h * a.k.sh, a.k.st, wave, lane, true);
     vl.init(a.v.ptr + b * a.v.sb + h * a.v.sh, a.v.st, wave, lane, false);
+    // K0, V0 (and K1) go out before the Q rows are read: the two latencies overlap
+    kl.issue(0, len, k_lds0, wave, lane);
+    vl.issue(0, len, v_lds0, wave, lane);
+    if (ntiles > 1) kl.issue(1, len, k_lds1, wave, lane);
+
+    bf16x8 qf[8];
+    load_q_fragment<QP>(a, b, h, qrow, hh, qf);
 
     const float sl2 = a.scale * kLog2e;
 
@@ -396,10 +400,7 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
       __syncthreads();
     };
 
-    // prologue: K0, V0 (and K1) -> S(0)
-    kl.issue(0, len, k_lds0, wave, lane);
-    vl.issue(0, len, v_lds0, wave, lane);
-    if (ntiles > 1) kl.issue(1, len, k_lds1, wave, lane);
+    // prologue: S(0) once K0, V0, K1 have landed
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     f32x16 sa0, sa1, sb0, sb1;
@@ -451,16 +452,29 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
 template __global__ void flash_fwd_kernel<kWaves, kQPlain>(const FlashArgs);
 template __global__ void flash_fwd_kernel<kWaves, kQNorm>(const FlashArgs);
 template __global__ void flash_fwd_kernel<kWaves, kQNormRope>(const FlashArgs);
+template __global__ void flash_fwd_kernel<4, kQPlain>(const FlashArgs);
+template __global__ void flash_fwd_kernel<4, kQNorm>(const FlashArgs);
+template __global__ void flash_fwd_kernel<4, kQNormRope>(const FlashArgs);
 
-template <int QP>
-int launch_qp(const FlashArgs& a, hipStream_t s) {
-  constexpr int BM = kWaves * 32;
+template <int NW, int QP>
+int launch_nw(const FlashArgs& a, hipStream_t s) {
+  constexpr int BM = NW * 32;
   const int64_t num_m = (a.Lq + BM - 1) / BM;
   const int64_t grid = num_m * a.B * a.H;
   if (grid > 0x7fffffff) return set_error(2, "flash_fwd: grid of %lld workgroups too large", (long long)grid);
-  hipLaunchKernelGGL((flash_fwd_kernel<kWaves, QP>), dim3((unsigned)grid), dim3(kWaves * 64), 0, s, a);
+  hipLaunchKernelGGL((flash_fwd_kernel<NW, QP>), dim3((unsigned)grid), dim3(NW * 64), 0, s, a);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? 0 : set_error(4, "flash_fwd launch: %s", hipGetErrorString(e));
+}
+
+#ifndef WAN_SHORT_KEYS
+#define WAN_SHORT_KEYS 1024
+#endif
+
+template <int QP>
+int launch_qp(const FlashArgs& a, hipStream_t s) {
+  if (a.Lk <= WAN_SHORT_KEYS) return launch_nw<4, QP>(a, s);
+  return launch_nw<kWaves, QP>(a, s);
 }
 
 }  // namespace
