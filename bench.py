@@ -75,7 +75,7 @@ def make_inputs(torch, grid, seed, dev):
 
 
 class FusedSelf:
-    """One step = wan_rms_norm(q: statistics) + wan_rms_norm(k: norm+rope) + attention with
+    """One step = wan_rms_norm_qk (q statistics + k norm/rope, one launch) + attention with
     the q norm/rope in the kernel; buffers allocated once, outside the timed region."""
 
     def __init__(self, torch, W, t):
@@ -91,11 +91,10 @@ class FusedSelf:
 
     def prep(self):
         t, N, lib = self.t, self.N, self.lib
-        N.check("q stats", lib.wan_rms_norm(N.tensor4(t["q"]), None, self.Bn, self.L, H, D, None, 1e-6,
-                                            None, None, self.inv.data_ptr(), self.stream))
-        N.check("k prep", lib.wan_rms_norm(N.tensor4(t["k"]), self.khat.data_ptr(), self.Bn, self.L, H, D,
-                                           t["gk"].data_ptr(), 1e-6, t["cos"].data_ptr(),
-                                           t["sin"].data_ptr(), None, self.stream))
+        N.check("qk prep", lib.wan_rms_norm_qk(N.tensor4(t["q"]), N.tensor4(t["k"]), self.khat.data_ptr(),
+                                               self.Bn, self.L, H, D, t["gk"].data_ptr(), 1e-6,
+                                               t["cos"].data_ptr(), t["sin"].data_ptr(),
+                                               self.inv.data_ptr(), self.stream))
 
     def attn(self):
         t, N, lib = self.t, self.N, self.lib

@@ -128,6 +128,17 @@ int wan_rms_norm(wan_tensor x, void* out, int batch, int seqlen, int heads, int 
                  float* inv_rms_out, void* stream);
 
 /*
+ * The two RMSNorm passes of a fused self-attention in one launch, as
+ * _tp_rms_qk treats q and k together (models/fast_dit.py:134-147, TP=1):
+ * inv_rms_q (fp32 [B*L]) = 1/rms of each q token over heads*128 channels, and
+ * k_out ([B, L, H, 128] contiguous) = rope(bf16(bf16(k * inv_rms_k) * gamma_k))
+ * as wan_rms_norm computes it (rope_cos/rope_sin NULL: no rotation).
+ */
+int wan_rms_norm_qk(wan_tensor q, wan_tensor k, void* k_out, int batch, int seqlen, int heads,
+                    int head_dim, const void* gamma_k, float eps, const float* rope_cos,
+                    const float* rope_sin, float* inv_rms_q, void* stream);
+
+/*
  * Attention whose query is normalised inside the kernel as it is loaded:
  *   q' = rope?(bf16(bf16(q * inv_rms_q[b, i]) * gamma_q)),  out = softmax(q' k^T * scale) v
  * with inv_rms_q from wan_rms_norm (fp32 [B*Lq]).  rope_cos/rope_sin NULL: no

@@ -197,6 +197,33 @@ def test_fused_equals_standalone_ops(W):
     assert torch.equal(fused, plain)
 
 
+def test_rms_norm_qk_equals_two_passes(W):
+    """wan_rms_norm_qk (one launch) == wan_rms_norm(q: statistics) + wan_rms_norm(k: norm+rope),
+    bit for bit, on strided [B, L, 3072] views at the config C width."""
+    N = W._native
+    lib = N.lib()
+    B, H, grid = 2, 24, (3, 7, 9)
+    L = grid[0] * grid[1] * grid[2]
+    x = _bf((B, L, 3 * H * D), 31).to(DEV)
+    q, k = x[..., :H * D].view(B, L, H, D), x[..., H * D:2 * H * D].view(B, L, H, D)
+    gk = _gammas(H * D, 32, True).to(DEV)
+    cos, sin = (t.to(DEV) for t in ref.rope_tables(ref.wan_freqs(D), grid, D))
+    s = torch.cuda.current_stream().cuda_stream
+    inv1, inv2 = (torch.empty(B * L, dtype=torch.float32, device=DEV) for _ in range(2))
+    k1, k2 = (torch.empty(B, L, H, D, dtype=torch.bfloat16, device=DEV) for _ in range(2))
+    N.check("qk", lib.wan_rms_norm_qk(N.tensor4(q), N.tensor4(k), k1.data_ptr(), B, L, H, D,
+                                      gk.data_ptr(), 1e-6, cos.data_ptr(), sin.data_ptr(),
+                                      inv1.data_ptr(), s))
+    N.check("q", lib.wan_rms_norm(N.tensor4(q), None, B, L, H, D, None, 1e-6, None, None,
+                                  inv2.data_ptr(), s))
+    N.check("k", lib.wan_rms_norm(N.tensor4(k), k2.data_ptr(), B, L, H, D, gk.data_ptr(), 1e-6,
+                                  cos.data_ptr(), sin.data_ptr(), None, s))
+    torch.cuda.synchronize()
+    assert torch.equal(inv1, inv2) and torch.equal(k1, k2)
+    want = ref.inv_rms(q.cpu().reshape(B, L, H * D).float())
+    assert torch.allclose(inv1.cpu().view(B, L), want.view(B, L), rtol=1e-5)
+
+
 def test_rope_bit_exact(W):
     B, H, grid = 2, 24, (4, 6, 8)
     L = grid[0] * grid[1] * grid[2]

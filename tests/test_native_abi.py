@@ -74,6 +74,13 @@ def test_validation_rejects_bad_arguments_without_launching(W):
     rc = lib.wan_flash_attn_qnorm(ok, ok, ok, ok, 1, 24, 16, 16, 128, None, 256, None, None, 0.1,
                                   None, None)
     assert rc == 1 and "inv_rms_q" in N.last_error()
+    # rms_norm_qk: both outputs are required; k's gamma is required with an output
+    rc = lib.wan_rms_norm_qk(ok, ok, None, 1, 16, 24, 128, 256, 1e-6, 256, 256, 256, None)
+    assert rc == 1 and "required" in N.last_error()
+    rc = lib.wan_rms_norm_qk(ok, ok, 256, 1, 16, 24, 128, None, 1e-6, 256, 256, 256, None)
+    assert rc == 1 and "gamma" in N.last_error()
+    rc = lib.wan_rms_norm_qk(ok, ok, 256, 1, 16, 24, 64, 256, 1e-6, 256, 256, 256, None)
+    assert rc == 2 and "head_dim" in N.last_error()
     # nothing to do is not an error
     assert lib.wan_flash_self_attn(ok, ok, ok, ok, 0, 24, 16, 16, 128, 0.1, 0, None) == 0
 

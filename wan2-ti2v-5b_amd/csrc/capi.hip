@@ -47,6 +47,34 @@ int check_dims(const char* fn, int B, int H, int Lq, int Lk, int D) {
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
+// Validates the arguments of one RMSNorm / statistics task and fills its PrepArgs.
+int rms_prep_args(const char* fn, wan_tensor x, void* out, int batch, int seqlen, int heads,
+                  int head_dim, const void* gamma, float eps, const float* rope_cos,
+                  const float* rope_sin, float* inv_rms_out, PrepArgs* a) {
+  int rc;
+  if ((rc = check_dims(fn, batch, heads, seqlen, seqlen, head_dim))) return rc;
+  if ((rc = check_tensor(fn, "x", x, batch, seqlen, heads))) return rc;
+  if (out && !aligned16(out)) return set_error(WAN_ERR_INVALID, "%s: out must be 16-byte aligned", fn);
+  if (out && (!gamma || !aligned16(gamma)))
+    return set_error(WAN_ERR_INVALID, "%s: gamma must be a 16-byte aligned pointer", fn);
+  if ((rope_cos == nullptr) != (rope_sin == nullptr))
+    return set_error(WAN_ERR_INVALID, "%s: rope_cos and rope_sin must both be given or both NULL", fn);
+  if (rope_cos && (!out || !aligned16(rope_cos) || !aligned16(rope_sin)))
+    return set_error(WAN_ERR_INVALID, "%s: rotation needs `out` and 16-byte aligned tables", fn);
+  if (!(eps >= 0.f)) return set_error(WAN_ERR_INVALID, "%s: eps must be >= 0", fn);
+  a->x = as_t4(x);
+  a->B = batch;
+  a->L = seqlen;
+  a->H = heads;
+  a->eps = eps;
+  a->inv_rms = inv_rms_out;
+  a->gamma = static_cast<const bf16*>(gamma);
+  a->cos = rope_cos;
+  a->sin = rope_sin;
+  a->out = static_cast<bf16*>(out);
+  return WAN_OK;
+}
+
 }  // namespace
 
 int set_error(int code, const char* fmt, ...) {
@@ -140,31 +168,31 @@ size_t wan_self_attn_fused_workspace(int batch, int heads, int seqlen) {
 int wan_rms_norm(wan_tensor x, void* out, int batch, int seqlen, int heads, int head_dim,
                  const void* gamma, float eps, const float* rope_cos, const float* rope_sin,
                  float* inv_rms_out, void* stream) {
-  const char* fn = "wan_rms_norm";
-  int rc;
-  if ((rc = check_dims(fn, batch, heads, seqlen, seqlen, head_dim))) return rc;
-  if ((rc = check_tensor(fn, "x", x, batch, seqlen, heads))) return rc;
-  if ((int64_t)batch * seqlen * heads == 0) return WAN_OK;
-  if (out && !aligned16(out)) return set_error(WAN_ERR_INVALID, "%s: out must be 16-byte aligned", fn);
-  if (out && (!gamma || !aligned16(gamma)))
-    return set_error(WAN_ERR_INVALID, "%s: gamma must be a 16-byte aligned pointer", fn);
-  if ((rope_cos == nullptr) != (rope_sin == nullptr))
-    return set_error(WAN_ERR_INVALID, "%s: rope_cos and rope_sin must both be given or both NULL", fn);
-  if (rope_cos && (!out || !aligned16(rope_cos) || !aligned16(rope_sin)))
-    return set_error(WAN_ERR_INVALID, "%s: rotation needs `out` and 16-byte aligned tables", fn);
-  if (!(eps >= 0.f)) return set_error(WAN_ERR_INVALID, "%s: eps must be >= 0", fn);
   PrepArgs a{};
-  a.x = as_t4(x);
-  a.B = batch;
-  a.L = seqlen;
-  a.H = heads;
-  a.eps = eps;
-  a.inv_rms = inv_rms_out;
-  a.gamma = static_cast<const bf16*>(gamma);
-  a.cos = rope_cos;
-  a.sin = rope_sin;
-  a.out = static_cast<bf16*>(out);
+  int rc;
+  if ((rc = rms_prep_args("wan_rms_norm", x, out, batch, seqlen, heads, head_dim, gamma, eps,
+                          rope_cos, rope_sin, inv_rms_out, &a)))
+    return rc;
+  if ((int64_t)batch * seqlen * heads == 0) return WAN_OK;
   return launch_rms_prep(a, static_cast<hipStream_t>(stream));
+}
+
+int wan_rms_norm_qk(wan_tensor q, wan_tensor k, void* k_out, int batch, int seqlen, int heads,
+                    int head_dim, const void* gamma_k, float eps, const float* rope_cos,
+                    const float* rope_sin, float* inv_rms_q, void* stream) {
+  const char* fn = "wan_rms_norm_qk";
+  if (inv_rms_q == nullptr || k_out == nullptr)
+    return set_error(WAN_ERR_INVALID, "%s: inv_rms_q and k_out are required", fn);
+  PrepArgs aq{}, ak{};
+  int rc;
+  if ((rc = rms_prep_args(fn, q, nullptr, batch, seqlen, heads, head_dim, nullptr, eps, nullptr,
+                          nullptr, inv_rms_q, &aq)))
+    return rc;
+  if ((rc = rms_prep_args(fn, k, k_out, batch, seqlen, heads, head_dim, gamma_k, eps, rope_cos,
+                          rope_sin, nullptr, &ak)))
+    return rc;
+  if ((int64_t)batch * seqlen * heads == 0) return WAN_OK;
+  return launch_rms_prep2(aq, ak, static_cast<hipStream_t>(stream));
 }
 
 int wan_flash_attn_qnorm(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor out, int batch,
@@ -237,11 +265,8 @@ int wan_self_attn_fused(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor out
   float* inv_q = static_cast<float*>(workspace);
   void* khat = static_cast<char*>(workspace) + align_up(rows * sizeof(float));
   const wan_tensor kt{khat, (int64_t)seqlen * heads * kHeadDim, (int64_t)heads * kHeadDim, kHeadDim};
-  if ((rc = wan_rms_norm(q, nullptr, batch, seqlen, heads, head_dim, nullptr, eps, nullptr,
-                         nullptr, inv_q, stream)))
-    return rc;
-  if ((rc = wan_rms_norm(k, khat, batch, seqlen, heads, head_dim, gamma_k, eps, rope_cos, rope_sin,
-                         nullptr, stream)))
+  if ((rc = wan_rms_norm_qk(q, k, khat, batch, seqlen, heads, head_dim, gamma_k, eps, rope_cos,
+                            rope_sin, inv_q, stream)))
     return rc;
   return wan_flash_attn_qnorm(q, kt, v, out, batch, heads, seqlen, seqlen, head_dim, inv_q, gamma_q,
                               rope_cos, rope_sin, softmax_scale, nullptr, stream);

@@ -64,6 +64,8 @@ struct PrepArgs {
   bf16* out;            // out [B, L, H, 128] contiguous (null: statistics only)
 };
 int launch_rms_prep(const PrepArgs& a, hipStream_t s);
+// Two tasks with the same H in one launch.
+int launch_rms_prep2(const PrepArgs& a0, const PrepArgs& a1, hipStream_t s);
 
 struct RopeArgs {
   Tensor4 x;

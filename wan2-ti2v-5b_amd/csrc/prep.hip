@@ -37,9 +37,9 @@ __device__ __forceinline__ void rope8(float u[8], const float* cos_row,
 // optionally the normalised (and rotated) row.  NCH: 8-channel chunks per lane
 // (H*16 <= 64*NCH), so the row's loads are issued unconditionally together.
 template <int NCH>
-__global__ __launch_bounds__(256) void rms_prep_kernel(const PrepArgs a) {
+__device__ __forceinline__ void rms_prep_rows(const PrepArgs& a, int block) {
   const int lane = threadIdx.x & 63;
-  const int tok = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int tok = block * 4 + (threadIdx.x >> 6);
   if (tok >= a.B * a.L) return;
   const int b = tok / a.L, l = tok - b * a.L;
   const int nchunks = a.H * 16;
@@ -89,6 +89,20 @@ __global__ __launch_bounds__(256) void rms_prep_kernel(const PrepArgs a) {
   }
 }
 
+template <int NCH>
+__global__ __launch_bounds__(256) void rms_prep_kernel(const PrepArgs a) {
+  rms_prep_rows<NCH>(a, blockIdx.x);
+}
+
+// Two independent tasks (the q statistics and the k norm + rotation of one
+// self-attention call) in one launch: blocks [0, blocks0) run a0, the rest a1.
+template <int NCH>
+__global__ __launch_bounds__(256) void rms_prep2_kernel(const PrepArgs a0, const PrepArgs a1, int blocks0) {
+  if ((int)blockIdx.x < blocks0) rms_prep_rows<NCH>(a0, blockIdx.x);
+  else rms_prep_rows<NCH>(a1, blockIdx.x - blocks0);
+}
+
+
 // One thread per 8 channels: out = rope(x), the _rope semantics on its own.
 __global__ __launch_bounds__(256) void rope_kernel(const RopeArgs a) {
   const int64_t chunk = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -126,6 +140,25 @@ int launch_rms_prep(const PrepArgs& a, hipStream_t s) {
   else if (nch <= 384) hipLaunchKernelGGL(rms_prep_kernel<6>, grid, block, 0, s, a);
   else if (nch <= 512) hipLaunchKernelGGL(rms_prep_kernel<8>, grid, block, 0, s, a);
   else hipLaunchKernelGGL(rms_prep_kernel<16>, grid, block, 0, s, a);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : set_error(4, "rms_prep launch: %s", hipGetErrorString(e));
+}
+
+int launch_rms_prep2(const PrepArgs& a0, const PrepArgs& a1, hipStream_t s) {
+  if (a0.H != a1.H) return set_error(1, "rms_prep: the paired tasks differ in heads");
+  const int rows0 = a0.B * a0.L, rows1 = a1.B * a1.L;
+  if (rows0 == 0) return launch_rms_prep(a1, s);
+  if (rows1 == 0) return launch_rms_prep(a0, s);
+  const int nch = a0.H * 16;
+  if (nch > 64 * kMaxChunksPerLane) return set_error(2, "rms_prep: H*128=%d channels exceeds 8192", a0.H * 128);
+  const int blocks0 = (rows0 + 3) / 4;
+  const dim3 grid(blocks0 + (rows1 + 3) / 4), block(256);
+  if (nch <= 64) hipLaunchKernelGGL(rms_prep2_kernel<1>, grid, block, 0, s, a0, a1, blocks0);
+  else if (nch <= 128) hipLaunchKernelGGL(rms_prep2_kernel<2>, grid, block, 0, s, a0, a1, blocks0);
+  else if (nch <= 256) hipLaunchKernelGGL(rms_prep2_kernel<4>, grid, block, 0, s, a0, a1, blocks0);
+  else if (nch <= 384) hipLaunchKernelGGL(rms_prep2_kernel<6>, grid, block, 0, s, a0, a1, blocks0);
+  else if (nch <= 512) hipLaunchKernelGGL(rms_prep2_kernel<8>, grid, block, 0, s, a0, a1, blocks0);
+  else hipLaunchKernelGGL(rms_prep2_kernel<16>, grid, block, 0, s, a0, a1, blocks0);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? 0 : set_error(4, "rms_prep launch: %s", hipGetErrorString(e));
 }
