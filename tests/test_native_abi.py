@@ -50,6 +50,10 @@ def test_validation_rejects_bad_arguments_without_launching(W):
     bad = N.WanTensor(64, 24 * 128 * 16, 24 * 128 + 4, 128)
     rc = lib.wan_flash_self_attn(ok, bad, ok, ok, 1, 24, 16, 16, 128, 0.1, 0, None)
     assert rc == 1 and "stride" in N.last_error()
+    # token stride too large for the tile loader's 32-bit offsets
+    bad = N.WanTensor(64, 24 * 128 * 16, 1 << 24, 128)
+    rc = lib.wan_flash_self_attn(ok, bad, ok, ok, 1, 24, 16, 16, 128, 0.1, 0, None)
+    assert rc == 2 and "token stride" in N.last_error()
     # actual_seqlen_k beyond the keys
     rc = lib.wan_flash_self_attn(ok, ok, ok, ok, 1, 24, 16, 16, 128, 0.1, 17, None)
     assert rc == 1 and "actual_seqlen_k" in N.last_error()

@@ -32,6 +32,10 @@ int check_tensor(const char* fn, const char* name, const wan_tensor& t, int B, i
                      (long long)t.batch_stride, (long long)t.token_stride, (long long)t.head_stride);
   if (t.batch_stride < 0 || t.token_stride < 0 || t.head_stride < 0)
     return set_error(WAN_ERR_INVALID, "%s: %s has a negative stride", fn, name);
+  // the attention tile loads keep row * token_stride of a 64-key tile in 32-bit byte offsets
+  if (t.token_stride >= (int64_t(1) << 24))
+    return set_error(WAN_ERR_UNSUPPORTED, "%s: %s token stride %lld exceeds 2^24 elements", fn, name,
+                     (long long)t.token_stride);
   return WAN_OK;
 }
 
