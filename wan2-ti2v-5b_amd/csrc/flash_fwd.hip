@@ -432,18 +432,38 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
 
   const float l_tot = pair_sum(l_run);
   const float inv_l = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  if (qrow < a.Lq) {
-    bf16* op = a.o + b * a.o_sb + (int64_t)qrow * a.o_st + h * a.o_sh;
+
+  // Output store, staged through LDS so that each store instruction writes
+  // whole 128-byte row segments (8 rows x 128 B) instead of 8-byte pieces of
+  // 32 rows.  The K buffers are free here: their last reads came before the
+  // last barrier, and no load into them is in flight.  Each wave owns 4 KB
+  // (32 rows x 64 channels) and writes its 128 channels in two halves; rows
+  // hold 8 chunks of 16 B, chunk c of row r at position c ^ (r & 7).
+  bf16* stage = (wave < 4 ? k_lds0 : k_lds1) + (wave & 3) * 2048;
+  const int row0 = mblk * BM + wave * 32;
+  bf16* obase = a.o + b * a.o_sb + h * a.o_sh;
 #pragma unroll
-    for (int md = 0; md < 4; ++md) {
+  for (int half = 0; half < 2; ++half) {
+#pragma unroll
+    for (int mm = 0; mm < 2; ++mm) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         bf16x4 w;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) w[e] = (bf16)(o[md][4 * g + e] * inv_l);
-        *reinterpret_cast<bf16x4*>(op + 32 * md + 8 * g + 4 * hh) = w;
+        for (int e = 0; e < 4; ++e) w[e] = (bf16)(o[2 * half + mm][4 * g + e] * inv_l);
+        const int c = 4 * mm + g;  // lane holds channels 8c + 4hh .. +3 of row n32
+        *reinterpret_cast<bf16x4*>(stage + n32 * 64 + ((c ^ (n32 & 7)) << 3) + 4 * hh) = w;
       }
     }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = 8 * j + (lane >> 3), c = lane & 7;
+      const bf16x8 v = *reinterpret_cast<const bf16x8*>(stage + r * 64 + ((c ^ (r & 7)) << 3));
+      if (row0 + r < a.Lq)
+        *reinterpret_cast<bf16x8*>(obase + (int64_t)(row0 + r) * a.o_st + 64 * half + 8 * c) = v;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }
 }
 
