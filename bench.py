@@ -14,7 +14,8 @@ attention, on seeded N(0,1) projections already resident in HBM.
   cpu_baseline  the oracle's torch SDPA (fp32) on the host cores, on a bounded sample
               of (batch, head) pairs of the same workload
   extra       the same path at L=1080 and the masked cross-attention (Lq=7854,
-              512 text keys, per-sample lengths U[16, 512]), with HBM GB/s; one
+              512 text keys, per-sample lengths U[16, 512]), with HBM GB/s; torch's
+              own flash SDPA on the config C shapes, for comparison; one
               WanAttentionBlock (D) and the 30-layer DiT, 10 UniPC steps (E):
               dit_s_per_step is the second half of the metric
 
@@ -160,6 +161,23 @@ def bench_cross(torch, W, dev, steps, warmup):
         "hbm_gbs_kernel": byts / (t_attn * 1e-3) / 1e9,
         "frac_hbm_peak": byts / (t_attn * 1e-3) / 1e9 / PEAK_HBM_GBS,
     }
+
+
+def bench_torch_sdpa(torch, t, steps, warmup):
+    """torch's own F.scaled_dot_product_attention (flash backend) on the config C shapes:
+    plain attention of the same q/k/v sizes (no norm, no rotation), for comparison."""
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    q, k, v = (t[n].transpose(1, 2).contiguous() for n in ("q", "k", "v"))
+    L = q.shape[2]
+    try:
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+            total, (ms,) = time_steps(torch, [lambda: F.scaled_dot_product_attention(q, k, v)], steps, warmup)
+    except RuntimeError as e:
+        return {"torch_sdpa_L7854": {"error": str(e)[:200]}}
+    return {"torch_sdpa_L7854": {
+        "workload": f"torch F.scaled_dot_product_attention, flash backend, B=2 H=24 L={L} d=128 bf16",
+        "ms": ms, "tflops": attn_flops(B, H, L, L) / (ms * 1e-3) / 1e12}}
 
 
 def bench_dit(torch, W, dev, steps, layers):
@@ -312,6 +330,7 @@ def main():
             "tflops_step": attn_flops(B, H, LA, LA) / (totA / args.steps * 1e-3) / 1e12,
             "tflops_kernel": attn_flops(B, H, LA, LA) / (aA * 1e-3) / 1e12}
         extra["cross_attn"] = bench_cross(torch, W, dev, args.steps, args.warmup)
+        extra.update(bench_torch_sdpa(torch, t, min(args.steps, 20), 3))
         log(f"extra: {json.dumps(extra)}")
     if not args.no_dit:
         extra.update(bench_dit(torch, W, dev, args.dit_steps, args.dit_layers))

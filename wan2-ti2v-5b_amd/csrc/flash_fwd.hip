@@ -33,7 +33,9 @@
 //    loads of tiles j+1 (V) and j+2 (K) are in flight.  One barrier per tile.
 //    In program order the S^T MFMAs of tile j+1 alternate with the exp2 /
 //    convert / sum of tile j (two MFMAs and four exponentials per k-step), and
-//    K and V^T operand fragments are read one MFMA ahead.
+//    K and V^T operand fragments are read one MFMA ahead.  The tile copies are
+//    issued from inline asm, out of sight of the compiler's wait counting, so
+//    the LDS operand reads wait only for themselves.
 //  * Q is loaded once per wave into registers; QK-RMSNorm (given the per-token
 //    inverse RMS) and the 3D-RoPE rotation are applied there, with the
 //    reference's bf16 rounding points (models/fast_dit.py:145-146,169).
@@ -130,6 +132,25 @@ __device__ __forceinline__ void load_q_fragment(const FlashArgs& a, int b, int h
   }
 }
 
+// 16-byte global -> LDS copies (global_load_lds_dwordx4): lane l writes LDS
+// bytes m0 + 16 l .. +15.  Issued from inline asm so that the compiler's
+// wait-count bookkeeping does not see them: it would otherwise treat every LDS
+// read that follows an in-flight copy as out of order and wait for all of
+// them (lgkmcnt(0)) before each use.  Completion is the kernel's own business:
+// every tile is waited for (s_waitcnt vmcnt(0)) before the barrier that
+// publishes it.  m0 is written here only; nothing else in the kernel uses it.
+__device__ __forceinline__ uint32_t lds_addr(const bf16* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) bf16*)p;
+}
+__device__ __forceinline__ void dma16_saddr(const char* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :: "s"(lds), "v"(voff), "s"(sbase) : "memory");
+}
+__device__ __forceinline__ void dma16_vaddr(const char* vaddr, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :: "s"(lds), "v"(vaddr) : "memory");
+}
+
 template <int NW>
 struct TileLoader {
   // Wave `wave` issues the 1 KB blocks i = wave, wave + NW, ... of a 16 KB
@@ -171,17 +192,15 @@ struct TileLoader {
       for (int u = 0; u < kPerWave; ++u) {
         // keep the 32 -> 64-bit extension next to the load (not hoisted out of
         // the tile loop) so instruction selection sees sgpr + zext(vgpr)
-        uint32_t off = lane_off[u];
-        asm volatile("" : "+v"(off));
-        __builtin_amdgcn_global_load_lds(tb + off, dst + (wave + NW * u) * 512, 16, 0, 0);
+        dma16_saddr(tb, lane_off[u], lds_addr(dst + (wave + NW * u) * 512));
       }
     } else {
 #pragma unroll
       for (int u = 0; u < kPerWave; ++u) {
         const int row = row_of(wave, lane, u);
         const int key = min(k0 + row, len - 1);
-        __builtin_amdgcn_global_load_lds(base + ((int64_t)key * stride + col_of(row, lane)) * 2,
-                                         dst + (wave + NW * u) * 512, 16, 0, 0);
+        dma16_vaddr(base + ((int64_t)key * stride + col_of(row, lane)) * 2,
+                    lds_addr(dst + (wave + NW * u) * 512));
       }
     }
   }
@@ -191,9 +210,8 @@ template <int NW, int QP>
 __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a) {
   constexpr int BM = NW * 32;
 
-  // Four distinct LDS objects (not one array) so the compiler can prove that
-  // the asynchronous global->LDS writes into one buffer do not alias the
-  // operand reads from the other, and does not wait for them.
+  // Four LDS tiles: K and V, double-buffered.  After the last tile the K
+  // buffers stage the output.
   __shared__ __attribute__((aligned(1024))) bf16 k_lds0[kTileElems];
   __shared__ __attribute__((aligned(1024))) bf16 k_lds1[kTileElems];
   __shared__ __attribute__((aligned(1024))) bf16 v_lds0[kTileElems];
