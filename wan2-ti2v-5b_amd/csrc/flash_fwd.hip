@@ -456,7 +456,9 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
   // 32 rows.  The K buffers are free here: their last reads came before the
   // last barrier, and no load into them is in flight.  Each wave owns 4 KB
   // (32 rows x 64 channels) and writes its 128 channels in two halves; rows
-  // hold 8 chunks of 16 B, chunk c of row r at position c ^ (r & 7).
+  // hold 8 chunks of 16 B, chunk c of row r at position c ^ (r & 7).  The
+  // stores are non-temporal: the output is written once and not re-read here,
+  // so it should not displace the K/V lines that other workgroups still read.
   bf16* stage = (wave < 4 ? k_lds0 : k_lds1) + (wave & 3) * 2048;
   const int row0 = mblk * BM + wave * 32;
   bf16* obase = a.o + b * a.o_sb + h * a.o_sh;
@@ -479,7 +481,7 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
       const int r = 8 * j + (lane >> 3), c = lane & 7;
       const bf16x8 v = *reinterpret_cast<const bf16x8*>(stage + r * 64 + ((c ^ (r & 7)) << 3));
       if (row0 + r < a.Lq)
-        *reinterpret_cast<bf16x8*>(obase + (int64_t)(row0 + r) * a.o_st + 64 * half + 8 * c) = v;
+        __builtin_nontemporal_store(v, reinterpret_cast<bf16x8*>(obase + (int64_t)(row0 + r) * a.o_st + 64 * half + 8 * c));
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }
