@@ -284,8 +284,8 @@ def main():
                     help="only run 10 device-to-device copies of BYTES (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build runs all 24 heads and CFG batch 2 on a single "
-              f"MI355X and has no multi-GPU path (asked for --gpus {args.gpus}).", file=sys.stderr)
+        print(f"bench.py measures one GPU: the attention path runs all 24 heads and CFG batch 2 on "
+              f"a single MI355X and has no multi-GPU path (asked for --gpus {args.gpus}).", file=sys.stderr)
         sys.exit(2)
 
     sys.path.insert(0, ROOT)
