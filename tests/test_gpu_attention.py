@@ -314,3 +314,55 @@ def test_config_c_constant_v(W):
     want = c.float().expand(B, L, H, D)
     rel = ((out - want).abs() / want.abs().clamp_min(1e-3)).max()
     assert float(rel) <= 2 ** -7
+
+
+# ---------------------------------------------------------------------------
+# output placement and repeatability
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("B,Lq,Lk,H,lens", [(2, 300, 300, 3, None), (2, 1100, 1100, 2, None),
+                                            (2, 333, 77, 2, (77, 5))])
+def test_output_stays_inside_its_view(W, B, Lq, Lk, H, lens):
+    """The output tile is staged through LDS and written as whole row segments: into an
+    output that is a strided view of a larger buffer (32 rows before and after, one head
+    on either side), exactly the view's elements change.  Covers the 8-wave (1100 keys)
+    and 4-wave (300, 77 keys) kernels and a partial last query block."""
+    N, lib = W._native, W._native.lib()
+    q, k, v = _bf((B, Lq, H, D), 91), _bf((B, Lk, H, D), 92), _bf((B, Lk, H, D), 93)
+    big = torch.full((B, Lq + 64, H + 2, D), -7.0, dtype=torch.bfloat16, device=DEV)
+    view = big[:, 32:32 + Lq, 1:1 + H, :]
+    qd, kd, vd = _d(q, k, v)
+    s = torch.cuda.current_stream().cuda_stream
+    if lens is None:
+        N.check("wan_flash_self_attn", lib.wan_flash_self_attn(
+            N.tensor4(qd), N.tensor4(kd), N.tensor4(vd), N.tensor4(view), B, H, Lq, Lk, D, SCALE, 0, s))
+    else:
+        sk = torch.tensor(lens, dtype=torch.int32, device=DEV)
+        N.check("wan_cross_attn", lib.wan_cross_attn(
+            N.tensor4(qd), N.tensor4(kd), N.tensor4(vd), N.tensor4(view), B, H, Lq, Lk, D, SCALE,
+            sk.data_ptr(), s))
+    torch.cuda.synchronize()
+    host = big.cpu()
+    inside = torch.zeros(host.shape, dtype=torch.bool)
+    inside[:, 32:32 + Lq, 1:1 + H, :] = True
+    assert bool((host[~inside] == -7.0).all())
+    want = ref.sdpa(q.float(), k.float(), v.float(), seqlen_k=None if lens is None else list(lens))
+    assert ref.rel_rms(host[:, 32:32 + Lq, 1:1 + H, :], want) <= 5e-3
+
+
+def test_repeat_calls_bit_identical(W):
+    """No atomics and a fixed reduction order: repeated launches at full size return the
+    same bits (a missing wait or barrier between the tile copies and their readers would
+    show up here as run-to-run differences)."""
+    B, H, grid = 2, 24, (21, 17, 22)
+    L = grid[0] * grid[1] * grid[2]
+    g = torch.Generator(device=DEV).manual_seed(95)
+    q, k, v = (torch.randn(B, L, H, D, device=DEV, generator=g).to(torch.bfloat16) for _ in range(3))
+    gq, gk = _d(_gammas(H * D, 96, True), _gammas(H * D, 97, True))
+    cos, sin = _d(*ref.rope_tables(ref.wan_freqs(D), grid, D))
+    outs = [W.ops.self_attn_fused(q, k, v, gq, gk, 1e-6, cos, sin, SCALE) for _ in range(3)]
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    ck, cv = k[:, :512].contiguous(), v[:, :512].contiguous()
+    lens = torch.tensor([470, 123], dtype=torch.int32, device=DEV)
+    outs = [W.ops.cross_attn_fused(q, ck, cv, gq, 1e-6, lens, SCALE) for _ in range(3)]
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
