@@ -8,7 +8,7 @@
 // the per-sample key lengths of the cross-attention call site.
 //
 // Design (one workgroup = 8 waves = 256 query rows of one (batch, head); one
-// workgroup per CU at 256 VGPRs per wave):
+// workgroup per CU at up to 256 VGPRs per wave):
 //  * S^T = K Q^T on v_mfma_f32_32x32x16_bf16: the key axis is the MFMA row
 //    axis, so each lane holds ONE query row (lane % 32) and 32 of the 64 keys
 //    of a tile.  Row max / row sum are lane-local plus one exchange with the
@@ -30,7 +30,9 @@
 //    double-buffered, 16-byte chunks XOR-swizzled per row so the MFMA operand
 //    reads are bank-conflict free without padding.  Software pipeline: while
 //    the softmax of tile j runs on the VALU, the S^T MFMAs of tile j+1 and the
-//    loads of tiles j+1 (V) and j+2 (K) are in flight.  One barrier per tile.
+//    loads of tiles j+1 (V) and j+2 (K) are in flight.  One barrier per tile;
+//    with 8 waves a ring of four K and four V tiles (128 KB) lets the barrier
+//    come every second tile, the loads of a tile pair going out one pair ahead.
 //    In program order the S^T MFMAs of tile j+1 alternate with the exp2 /
 //    convert / sum of tile j (two MFMAs and four exponentials per k-step), and
 //    K and V^T operand fragments are read one MFMA ahead.  The tile copies are
@@ -210,12 +212,13 @@ template <int NW, int QP>
 __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a) {
   constexpr int BM = NW * 32;
 
-  // Four LDS tiles: K and V, double-buffered.  After the last tile the K
+  // K and V tiles resident per workgroup: a ring of four each (128 KB) with
+  // 8 waves, which run one workgroup per CU; two each (64 KB) with 4 waves, so
+  // that two workgroups fit a CU.  After the last tile the first two K
   // buffers stage the output.
-  __shared__ __attribute__((aligned(1024))) bf16 k_lds0[kTileElems];
-  __shared__ __attribute__((aligned(1024))) bf16 k_lds1[kTileElems];
-  __shared__ __attribute__((aligned(1024))) bf16 v_lds0[kTileElems];
-  __shared__ __attribute__((aligned(1024))) bf16 v_lds1[kTileElems];
+  constexpr int RING = NW == 8 ? 4 : 2;
+  __shared__ __attribute__((aligned(1024))) bf16 k_lds[RING][kTileElems];
+  __shared__ __attribute__((aligned(1024))) bf16 v_lds[RING][kTileElems];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -256,10 +259,14 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
     TileLoader<NW> kl, vl;
     kl.init(a.k.ptr + b * a.k.sb + h * a.k.sh, a.k.st, wave, lane, true);
     vl.init(a.v.ptr + b * a.v.sb + h * a.v.sh, a.v.st, wave, lane, false);
-    // K0, V0 (and K1) go out before the Q rows are read: the two latencies overlap
-    kl.issue(0, len, k_lds0, wave, lane);
-    vl.issue(0, len, v_lds0, wave, lane);
-    if (ntiles > 1) kl.issue(1, len, k_lds1, wave, lane);
+    // the first tiles go out before the Q rows are read: the two latencies overlap
+    kl.issue(0, len, k_lds[0], wave, lane);
+    vl.issue(0, len, v_lds[0], wave, lane);
+    if (ntiles > 1) kl.issue(1, len, k_lds[1], wave, lane);
+    if constexpr (RING == 4) {
+      if (ntiles > 1) vl.issue(1, len, v_lds[1], wave, lane);
+      if (ntiles > 2) kl.issue(2, len, k_lds[2], wave, lane);
+    }
 
     bf16x8 qf[8];
     load_q_fragment<QP>(a, b, h, qrow, hh, qf);
@@ -422,30 +429,71 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     f32x16 sa0, sa1, sb0, sb1;
-    qk(k_lds0, sa0, sa1);
+    qk(k_lds[0], sa0, sa1);
     __syncthreads();  // every wave is done with K0 before K2 overwrites it
 
     int t = 0;
-    for (; t + 2 < ntiles; t += 2) {
-      step(t, k_lds0, v_lds1, k_lds1, v_lds0, sa0, sa1, sb0, sb1);
-      step(t + 1, k_lds1, v_lds0, k_lds0, v_lds1, sb0, sb1, sa0, sa1);
-    }
-    // One full tile may remain before the last; then the last tile's scores are
-    // moved into sa so that a single copy of the last-tile code follows (its
-    // V buffer is picked at run time; every load has landed by then).
-    const bf16* v_last = v_lds0;
-    if (t + 1 < ntiles) {
-      step(t, k_lds0, v_lds1, k_lds1, v_lds0, sa0, sa1, sb0, sb1);
-      sa0 = sb0;
-      sa1 = sb1;
-      v_last = v_lds1;
-      ++t;
+    const bf16* v_last = v_lds[0];
+    if constexpr (RING == 2) {
+      for (; t + 2 < ntiles; t += 2) {
+        step(t, k_lds[0], v_lds[1], k_lds[1], v_lds[0], sa0, sa1, sb0, sb1);
+        step(t + 1, k_lds[1], v_lds[0], k_lds[0], v_lds[1], sb0, sb1, sa0, sa1);
+      }
+      // One full tile may remain before the last; then the last tile's scores are
+      // moved into sa so that a single copy of the last-tile code follows (its
+      // V buffer is picked at run time; every load has landed by then).
+      if (t + 1 < ntiles) {
+        step(t, k_lds[0], v_lds[1], k_lds[1], v_lds[0], sa0, sa1, sb0, sb1);
+        sa0 = sb0;
+        sa1 = sb1;
+        v_last = v_lds[1];
+        ++t;
+      }
+    } else {
+      // Ring of four: a barrier after every second step only.  An even step t
+      // issues the next pair's tiles, K(t+3), K(t+4), V(t+2), V(t+3), into the
+      // buffers that the previous pair finished reading; the odd step after it
+      // waits for them and publishes them with the barrier.
+      auto step4 = [&](int t, int odd, const bf16* k_next, const bf16* v_cur, bf16* kf3, bf16* kf4,
+                       bf16* vf2, bf16* vf3, f32x16& c0, f32x16& c1, f32x16& n0, f32x16& n1) {
+        if (!odd) {
+          if (t + 3 < ntiles) kl.issue(t + 3, len, kf3, wave, lane);
+          if (t + 4 < ntiles) kl.issue(t + 4, len, kf4, wave, lane);
+          if (t + 2 < ntiles) vl.issue(t + 2, len, vf2, wave, lane);
+          if (t + 3 < ntiles) vl.issue(t + 3, len, vf3, wave, lane);
+        }
+        bf16x8 pb[4];
+        finish(c0, c1, qk_exp(k_next, n0, n1, c0, c1, pb), pb);
+        pv(pb, v_cur);
+        if (odd) {
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+          __syncthreads();
+        }
+      };
+      for (; t + 4 < ntiles; t += 4) {
+        step4(t, 0, k_lds[1], v_lds[0], k_lds[3], k_lds[0], v_lds[2], v_lds[3], sa0, sa1, sb0, sb1);
+        step4(t + 1, 1, k_lds[2], v_lds[1], nullptr, nullptr, nullptr, nullptr, sb0, sb1, sa0, sa1);
+        step4(t + 2, 0, k_lds[3], v_lds[2], k_lds[1], k_lds[2], v_lds[0], v_lds[1], sa0, sa1, sb0, sb1);
+        step4(t + 3, 1, k_lds[0], v_lds[3], nullptr, nullptr, nullptr, nullptr, sb0, sb1, sa0, sa1);
+      }
+      // the remaining full tiles (at most three), buffers picked at run time
+      for (; t + 1 < ntiles; ++t) {
+        const int j = t & 3;
+        step4(t, t & 1, k_lds[(j + 1) & 3], v_lds[j], k_lds[(j + 3) & 3], k_lds[j], v_lds[(j + 2) & 3],
+              v_lds[(j + 3) & 3], sa0, sa1, sb0, sb1);
+        sa0 = sb0;
+        sa1 = sb1;
+      }
+      v_last = v_lds[t & 3];
     }
     // the last tile, its keys >= len masked when it is partial
     if (ntiles * BN > len) mask_tile(sa0, sa1, t * BN);
     bf16x8 pb[4];
     finish(sa0, sa1, exp_tile(sa0, sa1, pb), pb);
     pv(pb, v_last);
+    // the output staging below overwrites K buffers that a slower wave may
+    // still read in its last step when that step ended without a barrier
+    if constexpr (RING == 4) __syncthreads();
   }
 
   const float l_tot = pair_sum(l_run);
@@ -459,7 +507,7 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
   // hold 8 chunks of 16 B, chunk c of row r at position c ^ (r & 7).  The
   // stores are non-temporal: the output is written once and not re-read here,
   // so it should not displace the K/V lines that other workgroups still read.
-  bf16* stage = (wave < 4 ? k_lds0 : k_lds1) + (wave & 3) * 2048;
+  bf16* stage = (wave < 4 ? k_lds[0] : k_lds[1]) + (wave & 3) * 2048;
   const int row0 = mblk * BM + wave * 32;
   bf16* obase = a.o + b * a.o_sb + h * a.o_sh;
 #pragma unroll
