@@ -40,7 +40,10 @@
 //    the LDS operand reads wait only for themselves.
 //  * Q is loaded once per wave into registers; QK-RMSNorm (given the per-token
 //    inverse RMS) and the 3D-RoPE rotation are applied there, with the
-//    reference's bf16 rounding points (models/fast_dit.py:145-146,169).
+//    reference's bf16 rounding points (models/fast_dit.py:145-146,169).  The
+//    wave's 32 cos and sin rows come through LDS (1 KB copies, before the K/V
+//    tiles occupy it): read per lane from global memory they cost each wave
+//    512 scattered 32-byte requests.
 //  * Workgroup ids are remapped so each XCD owns contiguous query blocks of the
 //    same heads (K/V reuse in that XCD's L2); with per-sample key lengths the
 //    batch index varies fastest instead, balancing long and short samples
@@ -93,7 +96,8 @@ __device__ __forceinline__ int v_swz(int row) { return (row & 3) << 2; }
 // k-step ks, channels 16*ks + 8*hh .. +7 of query row `row`.
 template <int QP>
 __device__ __forceinline__ void load_q_fragment(const FlashArgs& a, int b, int h, int row,
-                                                int hh, bf16x8 qf[8]) {
+                                                int hh, bf16x8 qf[8], const char* cos_lds,
+                                                const char* sin_lds, int n32) {
   if (row >= a.Lq) {
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) qf[ks] = bf16x8{};
@@ -102,22 +106,30 @@ __device__ __forceinline__ void load_q_fragment(const FlashArgs& a, int b, int h
   const bf16* qp = a.q.ptr + b * a.q.sb + (int64_t)row * a.q.st + h * a.q.sh;
   float inv = 1.f;
   if (QP != kQPlain) inv = a.inv_rms_q[(int64_t)b * a.Lq + row];
+  bf16x8 x[8], g[8];
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) {
     const int d0 = 16 * ks + 8 * hh;
-    bf16x8 x = *reinterpret_cast<const bf16x8*>(qp + d0);
+    x[ks] = *reinterpret_cast<const bf16x8*>(qp + d0);
+    if (QP != kQPlain) g[ks] = *reinterpret_cast<const bf16x8*>(a.gamma_q + h * D + d0);
+  }
+  // the staged RoPE rows (copies issued by this wave before) have landed
+  if (QP == kQNormRope) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) {
     if (QP != kQPlain) {
 #pragma clang fp contract(off)
-      const bf16x8 g = *reinterpret_cast<const bf16x8*>(a.gamma_q + h * D + d0);
       float u[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const bf16 t = (bf16)((float)x[j] * inv);
-        u[j] = (float)(bf16)((float)t * (float)g[j]);
+        const bf16 t = (bf16)((float)x[ks][j] * inv);
+        u[j] = (float)(bf16)((float)t * (float)g[ks][j]);
       }
       if (QP == kQNormRope) {
-        const f32x4 c = *reinterpret_cast<const f32x4*>(a.cos + (int64_t)row * kRopePairs + d0 / 2);
-        const f32x4 s = *reinterpret_cast<const f32x4*>(a.sin + (int64_t)row * kRopePairs + d0 / 2);
+        // chunk (2 ks + hh) of row n32 sits at position chunk ^ (n32 & 15)
+        const int off = n32 * 256 + (((2 * ks + hh) ^ (n32 & 15)) << 4);
+        const f32x4 c = *reinterpret_cast<const f32x4*>(cos_lds + off);
+        const f32x4 s = *reinterpret_cast<const f32x4*>(sin_lds + off);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const float xr = u[2 * j], xi = u[2 * j + 1];
@@ -128,9 +140,9 @@ __device__ __forceinline__ void load_q_fragment(const FlashArgs& a, int b, int h
         }
       }
 #pragma unroll
-      for (int j = 0; j < 8; ++j) x[j] = (bf16)u[j];
+      for (int j = 0; j < 8; ++j) x[ks][j] = (bf16)u[j];
     }
-    qf[ks] = x;
+    qf[ks] = x[ks];
   }
 }
 
@@ -151,6 +163,22 @@ __device__ __forceinline__ void dma16_saddr(const char* sbase, uint32_t voff, ui
 __device__ __forceinline__ void dma16_vaddr(const char* vaddr, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
                :: "s"(lds), "v"(vaddr) : "memory");
+}
+
+// Copies rows [row0, row0 + 32) of a table with 256-byte rows into 8 KB of
+// LDS, 1 KB (four rows) per copy: chunk c of row r lands at position
+// c ^ (r & 15), so the per-lane 16-byte reads of one chunk across 16 rows
+// are conflict free.  Rows past last_row repeat last_row.
+__device__ __forceinline__ void stage_rows32(const char* base, int64_t row_bytes, int row0, int last_row,
+                                             bf16* lds, int lane) {
+  const uint32_t l0 = lds_addr(lds);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int rr = 4 * i + (lane >> 4);
+    const int row = min(row0 + rr, last_row);
+    const int c = (lane & 15) ^ (rr & 15);
+    dma16_vaddr(base + (int64_t)row * row_bytes + c * 16, l0 + i * 1024);
+  }
 }
 
 template <int NW>
@@ -259,7 +287,26 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
     TileLoader<NW> kl, vl;
     kl.init(a.k.ptr + b * a.k.sb + h * a.k.sh, a.k.st, wave, lane, true);
     vl.init(a.v.ptr + b * a.v.sb + h * a.v.sh, a.v.st, wave, lane, false);
-    // the first tiles go out before the Q rows are read: the two latencies overlap
+    // RoPE tables: this wave's 32 cos and sin rows go through LDS (the ring
+    // buffers are free until the first tiles are copied), read back per lane
+    bf16x8 qf[8];
+    if constexpr (QP == kQNormRope) {
+      const int row0w = mblk * BM + wave * 32;
+      bf16* cos_st = &k_lds[0][0] + wave * 4096;
+      bf16* sin_st = &v_lds[0][0] + wave * 4096;
+      stage_rows32(reinterpret_cast<const char*>(a.cos), kRopePairs * 4, row0w, a.Lq - 1, cos_st, lane);
+      stage_rows32(reinterpret_cast<const char*>(a.sin), kRopePairs * 4, row0w, a.Lq - 1, sin_st, lane);
+      load_q_fragment<QP>(a, b, h, qrow, hh, qf, reinterpret_cast<const char*>(cos_st),
+                          reinterpret_cast<const char*>(sin_st), n32);
+      // every wave's staging copies have landed (also those of a wave whose rows
+      // are all past Lq) and every wave is done reading them before the tiles
+      // are copied over them
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+    } else {
+      load_q_fragment<QP>(a, b, h, qrow, hh, qf, nullptr, nullptr, n32);
+    }
+    // the first tiles
     kl.issue(0, len, k_lds[0], wave, lane);
     vl.issue(0, len, v_lds[0], wave, lane);
     if (ntiles > 1) kl.issue(1, len, k_lds[1], wave, lane);
@@ -268,8 +315,6 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
       if (ntiles > 2) kl.issue(2, len, k_lds[2], wave, lane);
     }
 
-    bf16x8 qf[8];
-    load_q_fragment<QP>(a, b, h, qrow, hh, qf);
 
     const float sl2 = a.scale * kLog2e;
 
