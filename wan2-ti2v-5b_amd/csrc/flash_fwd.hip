@@ -247,6 +247,9 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
   constexpr int RING = NW == 8 ? 4 : 2;
   __shared__ __attribute__((aligned(1024))) bf16 k_lds[RING][kTileElems];
   __shared__ __attribute__((aligned(1024))) bf16 v_lds[RING][kTileElems];
+  // with the ring of four, 32 KB more: room for the RoPE row staging while
+  // the first K and V tiles are already being copied
+  __shared__ __attribute__((aligned(1024))) bf16 x_lds[RING == 4 ? 2 * kTileElems : 8];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -287,34 +290,54 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
     TileLoader<NW> kl, vl;
     kl.init(a.k.ptr + b * a.k.sb + h * a.k.sh, a.k.st, wave, lane, true);
     vl.init(a.v.ptr + b * a.v.sb + h * a.v.sh, a.v.st, wave, lane, false);
-    // RoPE tables: this wave's 32 cos and sin rows go through LDS (the ring
-    // buffers are free until the first tiles are copied), read back per lane
+    // RoPE tables: this wave's 32 cos and sin rows go through LDS and are read
+    // back per lane.  With the ring of four they use buffers 1-3 and the extra
+    // 32 KB while K0 and V0 are already being copied; with two buffers they use
+    // all of them and the tiles follow.
     bf16x8 qf[8];
     if constexpr (QP == kQNormRope) {
       const int row0w = mblk * BM + wave * 32;
-      bf16* cos_st = &k_lds[0][0] + wave * 4096;
-      bf16* sin_st = &v_lds[0][0] + wave * 4096;
+      bf16 *cos_st, *sin_st;
+      if constexpr (RING == 4) {
+        kl.issue(0, len, k_lds[0], wave, lane);
+        vl.issue(0, len, v_lds[0], wave, lane);
+        cos_st = wave < 6 ? &k_lds[1 + wave / 2][0] + (wave & 1) * 4096 : &x_lds[0] + (wave - 6) * 4096;
+        sin_st = wave < 6 ? &v_lds[1 + wave / 2][0] + (wave & 1) * 4096 : &x_lds[8192] + (wave - 6) * 4096;
+      } else {
+        cos_st = &k_lds[0][0] + wave * 4096;
+        sin_st = &v_lds[0][0] + wave * 4096;
+      }
       stage_rows32(reinterpret_cast<const char*>(a.cos), kRopePairs * 4, row0w, a.Lq - 1, cos_st, lane);
       stage_rows32(reinterpret_cast<const char*>(a.sin), kRopePairs * 4, row0w, a.Lq - 1, sin_st, lane);
       load_q_fragment<QP>(a, b, h, qrow, hh, qf, reinterpret_cast<const char*>(cos_st),
                           reinterpret_cast<const char*>(sin_st), n32);
       // every wave's staging copies have landed (also those of a wave whose rows
-      // are all past Lq) and every wave is done reading them before the tiles
-      // are copied over them
+      // are all past Lq) and every wave is done reading them before tiles are
+      // copied over them
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
+      if constexpr (RING == 4) {
+        if (ntiles > 1) {
+          kl.issue(1, len, k_lds[1], wave, lane);
+          vl.issue(1, len, v_lds[1], wave, lane);
+        }
+        if (ntiles > 2) kl.issue(2, len, k_lds[2], wave, lane);
+      } else {
+        kl.issue(0, len, k_lds[0], wave, lane);
+        vl.issue(0, len, v_lds[0], wave, lane);
+        if (ntiles > 1) kl.issue(1, len, k_lds[1], wave, lane);
+      }
     } else {
+      // the first tiles go out before the Q rows are read: the two latencies overlap
+      kl.issue(0, len, k_lds[0], wave, lane);
+      vl.issue(0, len, v_lds[0], wave, lane);
+      if (ntiles > 1) kl.issue(1, len, k_lds[1], wave, lane);
+      if constexpr (RING == 4) {
+        if (ntiles > 1) vl.issue(1, len, v_lds[1], wave, lane);
+        if (ntiles > 2) kl.issue(2, len, k_lds[2], wave, lane);
+      }
       load_q_fragment<QP>(a, b, h, qrow, hh, qf, nullptr, nullptr, n32);
     }
-    // the first tiles
-    kl.issue(0, len, k_lds[0], wave, lane);
-    vl.issue(0, len, v_lds[0], wave, lane);
-    if (ntiles > 1) kl.issue(1, len, k_lds[1], wave, lane);
-    if constexpr (RING == 4) {
-      if (ntiles > 1) vl.issue(1, len, v_lds[1], wave, lane);
-      if (ntiles > 2) kl.issue(2, len, k_lds[2], wave, lane);
-    }
-
 
     const float sl2 = a.scale * kLog2e;
 
@@ -470,12 +493,20 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
       __syncthreads();
     };
 
-    // prologue: S(0) once K0, V0, K1 have landed
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
     f32x16 sa0, sa1, sb0, sb1;
-    qk(k_lds[0], sa0, sa1);
-    __syncthreads();  // every wave is done with K0 before K2 overwrites it
+    if constexpr (QP == kQNormRope && RING == 4) {
+      // K0 and V0 were published by the staging barrier; K1, V1 and K2 land
+      // while S(0) is computed, and this barrier publishes them (and frees K0)
+      qk(k_lds[0], sa0, sa1);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+    } else {
+      // prologue: S(0) once the first tiles have landed
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      qk(k_lds[0], sa0, sa1);
+      __syncthreads();  // every wave is done with K0 before it is overwritten
+    }
 
     int t = 0;
     const bf16* v_last = v_lds[0];
