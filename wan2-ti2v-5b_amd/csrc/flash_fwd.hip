@@ -97,7 +97,8 @@ __device__ __forceinline__ int v_swz(int row) { return (row & 3) << 2; }
 template <int QP>
 __device__ __forceinline__ void load_q_fragment(const FlashArgs& a, int b, int h, int row,
                                                 int hh, bf16x8 qf[8], const char* cos_lds,
-                                                const char* sin_lds, int n32) {
+                                                const char* sin_lds, int n32,
+                                                const char* q_lds = nullptr) {
   if (row >= a.Lq) {
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) qf[ks] = bf16x8{};
@@ -110,11 +111,16 @@ __device__ __forceinline__ void load_q_fragment(const FlashArgs& a, int b, int h
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) {
     const int d0 = 16 * ks + 8 * hh;
-    x[ks] = *reinterpret_cast<const bf16x8*>(qp + d0);
+    if (q_lds == nullptr) x[ks] = *reinterpret_cast<const bf16x8*>(qp + d0);
     if (QP != kQPlain) g[ks] = *reinterpret_cast<const bf16x8*>(a.gamma_q + h * D + d0);
   }
-  // the staged RoPE rows (copies issued by this wave before) have landed
-  if (QP == kQNormRope) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // the staged rows (copies issued by this wave before) have landed
+  if (QP == kQNormRope || q_lds != nullptr) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (q_lds != nullptr) {
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+      x[ks] = *reinterpret_cast<const bf16x8*>(q_lds + n32 * 256 + (((2 * ks + hh) ^ (n32 & 15)) << 4));
+  }
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) {
     if (QP != kQPlain) {
@@ -327,15 +333,26 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
         vl.issue(0, len, v_lds[0], wave, lane);
         if (ntiles > 1) kl.issue(1, len, k_lds[1], wave, lane);
       }
+    } else if constexpr (RING == 2) {
+      // K0 and K1 go out first; the wave's 32 q rows come through the V
+      // buffers (1 KB copies instead of 32-row scattered loads), then V0
+      kl.issue(0, len, k_lds[0], wave, lane);
+      if (ntiles > 1) kl.issue(1, len, k_lds[1], wave, lane);
+      const int row0w = mblk * BM + wave * 32;
+      bf16* q_st = &v_lds[0][0] + wave * 4096;
+      stage_rows32(reinterpret_cast<const char*>(a.q.ptr + b * a.q.sb + h * a.q.sh), a.q.st * 2, row0w,
+                   a.Lq - 1, q_st, lane);
+      load_q_fragment<QP>(a, b, h, qrow, hh, qf, nullptr, nullptr, n32, reinterpret_cast<const char*>(q_st));
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();  // every wave is done with its staged rows before V0 lands there
+      vl.issue(0, len, v_lds[0], wave, lane);
     } else {
       // the first tiles go out before the Q rows are read: the two latencies overlap
       kl.issue(0, len, k_lds[0], wave, lane);
       vl.issue(0, len, v_lds[0], wave, lane);
       if (ntiles > 1) kl.issue(1, len, k_lds[1], wave, lane);
-      if constexpr (RING == 4) {
-        if (ntiles > 1) vl.issue(1, len, v_lds[1], wave, lane);
-        if (ntiles > 2) kl.issue(2, len, k_lds[2], wave, lane);
-      }
+      if (ntiles > 1) vl.issue(1, len, v_lds[1], wave, lane);
+      if (ntiles > 2) kl.issue(2, len, k_lds[2], wave, lane);
       load_q_fragment<QP>(a, b, h, qrow, hh, qf, nullptr, nullptr, n32);
     }
 
@@ -494,9 +511,10 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
     };
 
     f32x16 sa0, sa1, sb0, sb1;
-    if constexpr (QP == kQNormRope && RING == 4) {
-      // K0 and V0 were published by the staging barrier; K1, V1 and K2 land
-      // while S(0) is computed, and this barrier publishes them (and frees K0)
+    if constexpr ((QP == kQNormRope && RING == 4) || (QP != kQNormRope && RING == 2)) {
+      // the staging barrier published the first K tile(s) (and V0 with the
+      // ring of four); the tiles issued after it land while S(0) is computed,
+      // and this barrier publishes them and frees K0
       qk(k_lds[0], sa0, sa1);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
