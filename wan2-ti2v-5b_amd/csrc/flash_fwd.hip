@@ -43,7 +43,10 @@
 //    reference's bf16 rounding points (models/fast_dit.py:145-146,169).  The
 //    wave's 32 cos and sin rows come through LDS (1 KB copies, before the K/V
 //    tiles occupy it): read per lane from global memory they cost each wave
-//    512 scattered 32-byte requests.
+//    512 scattered 32-byte requests.  Without RoPE, the 4-wave kernel stages
+//    the q rows the same way.
+//  * The output tile goes back through LDS as well and leaves as whole 128-byte
+//    row segments, with non-temporal stores.
 //  * Workgroup ids are remapped so each XCD owns contiguous query blocks of the
 //    same heads (K/V reuse in that XCD's L2); with per-sample key lengths the
 //    batch index varies fastest instead, balancing long and short samples
