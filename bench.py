@@ -197,7 +197,7 @@ def bench_dit(torch, W, dev, steps, layers):
     torch.cuda.synchronize()
 
     # config D: one block, its inputs as in the DiT
-    e, e0 = fast._time_embed(torch.tensor(500))
+    e, e0 = fast.time_rows(torch.tensor(500))
     x = fast.patch(latent)
     ck, cv = fast.context[0]
     blk = fast.blocks[0]

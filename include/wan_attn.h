@@ -16,6 +16,8 @@
  *     allocates or frees device memory and never synchronises the stream.
  *   - `stream` is a hipStream_t (NULL = the null stream).  Every call is
  *     asynchronous and re-entrant.
+ *   - softmax_scale (every attention entry point) must be finite and > 0; other
+ *     values return WAN_ERR_UNSUPPORTED.
  *   - Return value: WAN_OK or an error code; wan_attn_last_error() returns the
  *     calling thread's last message.
  */

@@ -260,8 +260,8 @@ def block_forward(blk, x, e0, cos, sin, ck, cv, num_frames):
         return (per_frame(y) * g.unsqueeze(2)).view(B, L, C)
 
     def attn(q, k, v):
-        return F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2),
-                                              v.transpose(1, 2)).transpose(1, 2)
+        q, k, v = (t_.transpose(1, 2).contiguous() for t_ in (q, k, v))
+        return F.scaled_dot_product_attention(q, k, v).transpose(1, 2)
 
     h = mod(_ln32(x, blk.norm1), e[0], e[1])
     q = rope(_rms32(_lin32(h, sa.q), sa.norm_q).view(B, L, n, d), cos, sin)
@@ -286,23 +286,30 @@ def sinusoidal_embedding_1d(dim: int, position: torch.Tensor) -> torch.Tensor:
 
 def dit_forward(model, latent, t, ctx_cond, ctx_null, grid, guide_scale):
     """CFG noise prediction of the whole DiT in fp32 (ref_fp32.py:62-99): latent [C, F, H, W],
-    contexts [1, Lc, text_dim] -> [C_out, F, H, W]."""
+    contexts [1, Lc, text_dim] -> [C_out, F, H, W].
+
+    Runs on the device that holds the model's (fp32) weights; the RoPE tables, the
+    sinusoidal time embedding and the patch-embedding convolution are computed on the host
+    and moved there."""
     f, h, w = grid
     L = f * h * w
     dim, heads = model.dim, model.num_heads
     d = dim // heads
-    cos, sin = rope_tables(model.freqs, grid, d)
+    dev = model.head.head.weight.device
+    cos, sin = (t_.to(dev) for t_ in rope_tables(model.freqs, grid, d))
     t_frames = torch.full((f,), float(t), dtype=torch.float64)
     t_frames[0] = 0.0
     te = model.time_embedding
-    e = _lin32(F.silu(_lin32(sinusoidal_embedding_1d(model.freq_dim, t_frames).float(), te[0])), te[2])
+    s = sinusoidal_embedding_1d(model.freq_dim, t_frames).float().to(dev)
+    e = _lin32(F.silu(_lin32(s, te[0])), te[2])
     e = e.unsqueeze(0)                                              # [1, F, C]
     e0 = _lin32(F.silu(e), model.time_projection[1]).unflatten(2, (6, dim))
     tx = model.text_embedding
-    ctx = torch.cat([ctx_cond, ctx_null], 0).float()
+    ctx = torch.cat([ctx_cond, ctx_null], 0).float().to(dev)
     context = _lin32(F.gelu(_lin32(ctx, tx[0]), approximate="tanh"), tx[2])
     pe = model.patch_embedding
-    x = F.conv3d(latent.float().unsqueeze(0), pe.weight.float(), pe.bias.float(), stride=pe.stride)
+    x = F.conv3d(latent.float().cpu().unsqueeze(0), pe.weight.float().cpu(), pe.bias.float().cpu(),
+                 stride=pe.stride).to(dev)
     x = x.flatten(2).transpose(1, 2).expand(2, -1, -1).contiguous()
     for blk in model.blocks:
         ca = blk.cross_attn

@@ -105,12 +105,17 @@ def test_plain_self_ragged(W, B, Lq, Lk, H, actual):
     assert ref.rel_rms(out, want16) <= TOL_BF16
 
 
-@pytest.mark.parametrize("pattern,actual", [("rising", 0), ("falling", 0), ("jumps", 0), ("jumps", 937)])
-def test_large_logit_swings(W, pattern, actual):
+@pytest.mark.parametrize("pattern,actual,Lk", [
+    ("rising", 0, 1000), ("falling", 0, 1000), ("jumps", 0, 1000), ("jumps", 937, 1000),
+    # more than 1024 keys: the 8-wave kernel with its ring of four K/V tiles; 20 tiles leave
+    # the three-step remainder after the ring's groups of four, 2000 keys a partial last tile
+    ("rising", 0, 1280), ("falling", 0, 1280), ("jumps", 0, 1280), ("jumps", 0, 2000),
+    ("rising", 1990, 2000), ("jumps", 1217, 2000)])
+def test_large_logit_swings(W, pattern, actual, Lk):
     """Logits whose level moves by ~10-60 natural units between 64-key tiles (up to ~200:
     exp overflows without a reference max).  Exercises the exact-max rescale of O and l,
     which runs only when a tile's sum of p exceeds its bound."""
-    B, Lq, Lk, H = 1, 96, 1000, 2
+    B, Lq, H = 1, 96, 2
     g = torch.Generator().manual_seed(11)
     q = torch.randn(B, Lq, H, D, generator=g) * 0.3
     q[..., 0] = 1.0 + 0.1 * torch.randn(B, Lq, H, generator=g)
@@ -132,6 +137,63 @@ def test_large_logit_swings(W, pattern, actual):
     e = ref.rel_rms(out, want)
     print(f"{pattern} actual={actual}: rel_rms vs float64 {e:.3e}")
     assert torch.isfinite(out.float()).all() and e <= 5e-3
+
+
+@pytest.mark.parametrize("Lq,Lk,actual", [
+    (300, 1280, 0),      # 20 full tiles: ring groups of four plus the three-step remainder
+    (300, 1344, 0),      # 21 tiles: no remainder step before the last tile
+    (300, 1281, 0),      # 21 tiles, the last holds one key
+    (257, 2048, 0),      # 32 full tiles
+    (257, 2048, 1),      # one key
+    (257, 2048, 50),     # one partial tile
+    (257, 2048, 64),     # one full tile
+    (257, 2048, 128),    # two tiles
+    (257, 2048, 192),    # three tiles
+    (257, 2048, 250),    # four tiles, the last partial
+    (513, 1025, 1025),   # the smallest key count of the 8-wave kernel
+])
+def test_eight_wave_kernel_tile_counts(W, Lq, Lk, actual):
+    """Key counts above 1024 select the 8-wave kernel (256 query rows per workgroup, a ring
+    of four K and four V tiles, a barrier every second tile).  Every remainder of the ring
+    (tile counts 1-4 and 20, 21 = 0 and 1 mod 4, with 22/23 covered by L=1080 and 7854),
+    full and partial last tiles, against the fp32 and bf16 oracle."""
+    B, H = 2, 2
+    seed = 5000 + Lq + Lk + actual
+    q, k, v = _bf((B, Lq, H, D), seed), _bf((B, Lk, H, D), seed + 1), _bf((B, Lk, H, D), seed + 2)
+    out = W.ops.flash_self_attn(*_d(q, k, v), SCALE, actual).cpu()
+    n = actual if actual > 0 else Lk
+    assert torch.isfinite(out.float()).all()
+    assert ref.rel_rms(out, ref.sdpa(q.float(), k.float(), v.float(), seqlen_k=n)) <= 5e-3
+    assert ref.rel_rms(out, ref.sdpa(q, k, v, seqlen_k=n)) <= TOL_BF16
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_eight_wave_per_sample_lengths(W, fused):
+    """Per-sample key lengths and the in-kernel Q RMSNorm with more than 1024 keys (the
+    8-wave kernel): lengths 1, 130, 2000 and 0 in one batch, NaN in V and huge K past each
+    length, against the oracle; the length-0 sample is all zeros."""
+    B, H, Lq, Lk = 4, 3, 300, 2048
+    lens = [1, 130, 2000, 0]
+    q, ck, cv = _bf((B, Lq, H, D), 301), _bf((B, Lk, H, D), 302), _bf((B, Lk, H, D), 303)
+    gq = _gammas(H * D, 304, True)
+    ck2, cv2 = ck.clone(), cv.clone()
+    for b, n in enumerate(lens):
+        ck2[b, n:] = _bf((Lk - n, H, D), 310 + b, std=50.0)
+        cv2[b, n:] = float("nan")
+    sk = torch.tensor(lens, dtype=torch.int32).to(DEV)
+    if fused:
+        out = W.ops.cross_attn_fused(*_d(q, ck2, cv2, gq), 1e-6, sk, SCALE).cpu()
+        qn = ref.rms(q.reshape(B, Lq, H * D), gq).view(B, Lq, H, D)
+    else:
+        out = W.ops.cross_attn(*_d(q, ck2, cv2), sk, SCALE).cpu()
+        qn = q
+    assert torch.isfinite(out.float()).all()
+    assert torch.count_nonzero(out[3]) == 0
+    want = ref.sdpa(qn.float(), ck.float(), cv.float(), seqlen_k=lens)
+    for b in range(3):
+        e = ref.rel_rms(out[b], want[b])
+        print(f"fused={fused} len={lens[b]}: rel_rms vs fp32 {e:.3e}")
+        assert e <= 5e-3
 
 
 def test_single_key_returns_its_value(W):
@@ -286,8 +348,11 @@ def test_cross_masked_keys_do_not_matter(W):
 # full size self-attention (config C, L=7854 = grid 21x17x22)
 # ---------------------------------------------------------------------------
 
-def test_config_c_fused_sampled_heads(W):
-    B, H, grid = 2, 24, (21, 17, 22)
+@pytest.mark.parametrize("grid", [(21, 17, 22), (21, 22, 17)])
+def test_config_c_fused_sampled_heads(W, grid):
+    """L=7854 at the pipeline's latent grid (21, 17, 22) and at the reference block bench's
+    (21, 22, 17) (scripts/validate/block_bench.py:34): the same token count, other tables."""
+    B, H = 2, 24
     L = grid[0] * grid[1] * grid[2]
     q, k, v = _bf((B, L, H, D), 71), _bf((B, L, H, D), 72), _bf((B, L, H, D), 73)
     gq, gk = _gammas(H * D, 74, True), _gammas(H * D, 75, True)
@@ -297,7 +362,7 @@ def test_config_c_fused_sampled_heads(W):
     heads = [0, 13, 23]
     want = ref.sdpa(qr[:, :, heads].float(), kr[:, :, heads].float(), v[:, :, heads].float())
     e = ref.rel_rms(out[:, :, heads], want)
-    print(f"config C sampled heads {heads}: rel_rms vs fp32 {e:.3e}")
+    print(f"config C grid {grid} sampled heads {heads}: rel_rms vs fp32 {e:.3e}")
     assert e <= 5e-3
 
 

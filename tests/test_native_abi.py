@@ -156,3 +156,27 @@ def test_adaln_op_validates_on_cpu(W):
     xm = torch.empty(2, 12, 64, dtype=torch.bfloat16, device="meta")
     r, h = torch.ops.wan_hip.adaln(xm, xm, None, 3, -1, -1, -1, None, None, 1e-6, True)
     assert r.shape == xm.shape and h.shape == xm.shape
+
+
+@pytest.mark.parametrize("scale", [0.0, -0.088, float("inf"), float("nan")])
+def test_softmax_scale_must_be_finite_and_positive(W, scale):
+    """The kernels fold softmax_scale * log2(e) into one FMA per score and take the running
+    max over scaled scores: zero gives NaN on masked keys, a negative scale a wrong max.
+    Every attention entry point rejects such a scale before any work."""
+    N = W._native
+    lib = N.lib()
+    t = N.WanTensor(64, 24 * 128 * 16, 24 * 128, 128)
+    p = 256
+    calls = {
+        "wan_flash_self_attn": lambda: lib.wan_flash_self_attn(t, t, t, t, 1, 24, 16, 16, 128, scale, 0, None),
+        "wan_cross_attn": lambda: lib.wan_cross_attn(t, t, t, t, 1, 24, 16, 16, 128, scale, None, None),
+        "wan_flash_attn_qnorm": lambda: lib.wan_flash_attn_qnorm(t, t, t, t, 1, 24, 16, 16, 128, p, p, None,
+                                                                 None, scale, None, None),
+        "wan_self_attn_fused": lambda: lib.wan_self_attn_fused(t, t, t, t, 1, 24, 16, 128, p, p, 1e-6, p, p,
+                                                               scale, p, 1 << 30, None),
+        "wan_cross_attn_fused": lambda: lib.wan_cross_attn_fused(t, t, t, t, 1, 24, 16, 16, 128, p, 1e-6, scale,
+                                                                 None, p, 1 << 30, None),
+    }
+    for name, call in calls.items():
+        assert call() == 2, name
+        assert "softmax_scale" in N.last_error() and name in N.last_error()

@@ -92,3 +92,37 @@ def test_second_order_convergence_on_a_closed_form_ode(W):
     order_e = math.log2(errs[40][1] / errs[80][1])
     assert order_u > 1.8 and 0.8 < order_e < 1.2, (order_u, order_e)
     assert errs[40][0] < errs[40][1] / 50, errs
+
+
+def test_left_coefficients_round_like_zero_dim_promotion(W):
+    """Upstream multiplies tensors by 0-dim fp32 coefficients from the left; PyTorch rounds
+    such a coefficient to the tensor's dtype first (and keeps fp32 for one on the right).
+    The sampler hands its coefficients over as Python floats (kept at fp32 by the tensor
+    ops), pre-rounded by _left: the products must be the same bits as the 0-dim ones."""
+    from importlib import import_module
+    left = import_module(W.__name__ + ".unipc")._left
+    g = torch.Generator().manual_seed(4)
+    for dt in (torch.bfloat16, torch.float32):
+        t = torch.randn(4096, generator=g).to(dt)
+        for c in torch.rand(50, generator=g) * 3 - 1.5:
+            assert torch.equal(left(c, t) * t, c * t)
+    # the rounding matters: without it a bf16 product differs
+    t = torch.randn(4096, generator=g).to(torch.bfloat16)
+    c = torch.tensor(0.61237)
+    assert not torch.equal(float(c) * t, c * t)
+
+
+def test_bf16_sampler_keeps_dtype_and_lands_near_x0(W):
+    """The reference's loop runs the sampler on bf16 latents: every step returns bf16, and
+    with the exact straight-path velocity it still ends at x0 within bf16 rounding."""
+    g = torch.Generator().manual_seed(1)
+    x0 = torch.randn(4, 3, 5, 6, generator=g).bfloat16()
+    eps = torch.randn(4, 3, 5, 6, generator=g).bfloat16()
+    s = W.unipc.FlowUniPC(shift=1.0)
+    s.set_timesteps(10, shift=5.0)
+    x = ((1 - float(s.sigmas[0])) * x0.float() + float(s.sigmas[0]) * eps.float()).bfloat16()
+    for _ in range(10):
+        x = s.step((eps.float() - x0.float()).bfloat16(), x)
+        assert x.dtype == torch.bfloat16
+    assert float((x.float() - x0.float()).abs().max()) < 0.1
+    assert float((x.float() - x0.float()).pow(2).mean().sqrt()) < 2e-2

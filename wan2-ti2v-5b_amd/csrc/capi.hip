@@ -1,6 +1,7 @@
 // C-ABI entry points (include/wan_attn.h): argument validation, workspace
 // layout and dispatch to the kernels.  Nothing here allocates device memory
 // or synchronises the stream.
+#include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -50,6 +51,14 @@ int check_dims(const char* fn, int B, int H, int Lq, int Lk, int D) {
 }
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+// The kernels scale scores by softmax_scale * log2(e) and rely on that factor being
+// finite and positive (masked keys are -inf, the running max is a max of scaled scores).
+int check_scale(const char* fn, float scale) {
+  if (!(scale > 0.f) || !(scale < INFINITY))
+    return set_error(WAN_ERR_UNSUPPORTED, "%s: softmax_scale=%g, must be finite and > 0", fn, (double)scale);
+  return WAN_OK;
+}
 
 // Validates the arguments of one RMSNorm / statistics task and fills its PrepArgs.
 int rms_prep_args(const char* fn, wan_tensor x, void* out, int batch, int seqlen, int heads,
@@ -104,6 +113,7 @@ int wan_flash_self_attn(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor out
                         int actual_seqlen_k, void* stream) {
   const char* fn = "wan_flash_self_attn";
   int rc;
+  if ((rc = check_scale(fn, softmax_scale))) return rc;
   if ((rc = check_dims(fn, batch, heads, seqlen_q, seqlen_k, head_dim))) return rc;
   if ((rc = check_tensor(fn, "q", q, batch, seqlen_q, heads))) return rc;
   if ((rc = check_tensor(fn, "k", k, batch, seqlen_k, heads))) return rc;
@@ -139,6 +149,7 @@ int wan_cross_attn(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor out, int
                    const int32_t* seqlen_k_dev, void* stream) {
   const char* fn = "wan_cross_attn";
   int rc;
+  if ((rc = check_scale(fn, softmax_scale))) return rc;
   if ((rc = check_dims(fn, batch, heads, seqlen_q, seqlen_k, head_dim))) return rc;
   if ((rc = check_tensor(fn, "q", q, batch, seqlen_q, heads))) return rc;
   if ((rc = check_tensor(fn, "k", k, batch, seqlen_k, heads))) return rc;
@@ -206,6 +217,7 @@ int wan_flash_attn_qnorm(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor ou
                          void* stream) {
   const char* fn = "wan_flash_attn_qnorm";
   int rc;
+  if ((rc = check_scale(fn, softmax_scale))) return rc;
   if ((rc = check_dims(fn, batch, heads, seqlen_q, seqlen_k, head_dim))) return rc;
   if ((rc = check_tensor(fn, "q", q, batch, seqlen_q, heads))) return rc;
   if ((rc = check_tensor(fn, "k", k, batch, seqlen_k, heads))) return rc;
@@ -248,6 +260,7 @@ int wan_self_attn_fused(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor out
                         size_t workspace_bytes, void* stream) {
   const char* fn = "wan_self_attn_fused";
   int rc;
+  if ((rc = check_scale(fn, softmax_scale))) return rc;
   if ((rc = check_dims(fn, batch, heads, seqlen, seqlen, head_dim))) return rc;
   if ((rc = check_tensor(fn, "q", q, batch, seqlen, heads))) return rc;
   if ((rc = check_tensor(fn, "k", k, batch, seqlen, heads))) return rc;
@@ -288,6 +301,7 @@ int wan_cross_attn_fused(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor ou
                          void* workspace, size_t workspace_bytes, void* stream) {
   const char* fn = "wan_cross_attn_fused";
   int rc;
+  if ((rc = check_scale(fn, softmax_scale))) return rc;
   if ((rc = check_dims(fn, batch, heads, seqlen_q, seqlen_k, head_dim))) return rc;
   if ((rc = check_tensor(fn, "q", q, batch, seqlen_q, heads))) return rc;
   if ((rc = check_tensor(fn, "k", k, batch, seqlen_k, heads))) return rc;

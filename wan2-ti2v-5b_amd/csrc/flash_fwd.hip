@@ -161,17 +161,19 @@ __device__ __forceinline__ void load_q_fragment(const FlashArgs& a, int b, int h
 // read that follows an in-flight copy as out of order and wait for all of
 // them (lgkmcnt(0)) before each use.  Completion is the kernel's own business:
 // every tile is waited for (s_waitcnt vmcnt(0)) before the barrier that
-// publishes it.  m0 is written here only; nothing else in the kernel uses it.
+// publishes it.  The LDS address is an operand bound to m0 ("{m0}"), so the
+// compiler writes m0 itself and knows its value; the s_nop covers the wait
+// state between an m0 write and an LDS-DMA that reads it.
 __device__ __forceinline__ uint32_t lds_addr(const bf16* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) bf16*)p;
 }
 __device__ __forceinline__ void dma16_saddr(const char* sbase, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
-               :: "s"(lds), "v"(voff), "s"(sbase) : "memory");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
 }
 __device__ __forceinline__ void dma16_vaddr(const char* vaddr, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-               :: "s"(lds), "v"(vaddr) : "memory");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(vaddr), "{m0}"(lds) : "memory");
 }
 
 // Copies rows [row0, row0 + 32) of a table with 256-byte rows into 8 KB of

@@ -1,36 +1,33 @@
-"""Block-graph execution of the Wan DiT with a selectable attention backend.
+"""The Wan DiT forward around the attention path, on one GPU, with selectable backends.
 
-Mirrors models/fast_dit.py (the reference's fast path) at TP=1 with CFG as
-batch 2, on one GPU:
+This is the block-level drop-in for the reference's fast path (models/fast_dit.py) at
+TP=1, with classifier-free guidance run as batch 2 ([cond, uncond]).  The backends are
+chosen once at import, under the reference's selector names (models/fast_dit.py:43-45):
 
-  FAST_ATTN_IMPL   read once at import (models/fast_dit.py:43):
-                     "hip"  (default) the gfx950 kernels of this package: QK-RMSNorm and
-                            3D-RoPE fused into the flash self-attention, Q-RMSNorm fused
-                            into the masked cross-attention (ops.self_attn_fused,
-                            ops.cross_attn_fused)
-                     "sdpa" torch's F.scaled_dot_product_attention after separate
-                            QK-RMSNorm / RoPE ops (_sdpa, models/fast_dit.py:186-189)
-  FAST_CROSS_IMPL  cross-attention backend, defaults to FAST_ATTN_IMPL (:45, :299-304)
-  FAST_POINTWISE_IMPL  the block's pointwise chain (LayerNorms, _modulate, _gate, residual adds):
-                     "hip"  (default) one fused pass per stage (ops.adaln) and the FFN's
-                            tanh-GELU as the epilogue of its first GEMM
-                     "eager" the separate torch ops of models/fast_dit.py:280-311
+  FAST_ATTN_IMPL       "hip" (default): QK-RMSNorm, 3D-RoPE and the self-attention in the
+                       gfx950 kernels (ops.self_attn_fused); "sdpa": torch ops with the
+                       reference's rounding points and F.scaled_dot_product_attention
+  FAST_CROSS_IMPL      the cross-attention backend (default: FAST_ATTN_IMPL); "hip" runs the
+                       Q-RMSNorm + masked cross-attention kernel (ops.cross_attn_fused)
+  FAST_POINTWISE_IMPL  "hip" (default): each pointwise stage of a block is one fused pass
+                       (ops.adaln) and GELU is the FFN-up GEMM's epilogue; "eager": torch ops
 
-  _tp_rms_qk, _tp_rms  models/fast_dit.py:134-160 (TP=1: the all-reduce is the identity)
-  _rope                models/fast_dit.py:163-169
-  _modulate, _gate     models/fast_dit.py:172-181
-  _FastBlock           models/fast_dit.py:260-311
-  _FastCrossKV         models/fast_dit.py:464-477
-  _FastHead, _FastPatch, FastWanDiT   models/fast_dit.py:480-697
+A block (models/fast_dit.py:270-311) is organised here as four pointwise stages between
+its GEMM groups, e the block's per-frame modulation rows:
 
-Differences from the reference, all on purpose: no torch.compile (the
-reference compiles each block for Neuron; here the hot ops are hand-written
-kernels and the rest is eager PyTorch / hipBLASLt), the q/k/v projections of
-the "hip" path run as one GEMM on concatenated weights (the kernels read q, k, v
-as strided views of its output), cross-attention takes optional per-sample
-text lengths, and the patch embedding (a Conv3d whose stride equals its
-kernel) runs as the equivalent GEMM over gathered patches.
+  stage 1   h = LN1(x) * (1 + e1) + e0                 -> q/k/v, self-attention, O projection -> y
+  stage 2   x = x + y * e2;  h = LN3(x)                -> cross q, cross-attention, O         -> y
+  stage 3   x = x + y;       h = LN2(x) * (1 + e4) + e3 -> FFN up + GELU, FFN down           -> y
+  stage 4   x = x + y * e5
+
+Both pointwise implementations round to bf16 where the reference's eager graph does, and
+both attention backends see the same q, k, v.  Not done as the reference does: no
+torch.compile (the hot ops are hand-written kernels, the GEMMs hipBLASLt); with "hip" the
+q/k/v projections are one GEMM on concatenated weights, read by the kernels as strided
+views; cross-attention accepts per-sample text lengths; the patch embedding (a Conv3d with
+stride equal to its kernel) is the equivalent GEMM over gathered patches.
 """
+import math
 import os
 from typing import Optional, Sequence
 
@@ -52,53 +49,84 @@ if FAST_POINTWISE_IMPL not in ("hip", "eager"):
     raise ValueError(f"FAST_POINTWISE_IMPL={FAST_POINTWISE_IMPL!r}: expected 'hip' or 'eager'")
 
 
-def _lin(x, layer):
+def _linear(x, layer):
     return F.linear(x, layer.weight, layer.bias)
 
 
-def _tp_rms_qk(q, k, norm_q, norm_k):
-    """q [B, Lq, C], k [B, Lk, C]: RMS over all C channels, fp32 stats, bf16 roundings."""
-    qf, kf = q.float(), k.float()
-    C = q.shape[-1]
-    q_inv = torch.rsqrt(qf.pow(2).sum(-1, keepdim=True) / C + norm_q.eps)
-    k_inv = torch.rsqrt(kf.pow(2).sum(-1, keepdim=True) / C + norm_k.eps)
-    return (qf * q_inv).type_as(q) * norm_q.weight, (kf * k_inv).type_as(k) * norm_k.weight
+# ─── torch ops of the "sdpa" / "eager" side, rounding as the reference's graph ──────
 
-
-def _tp_rms(x, norm):
+def _rms_normalize(x, weight, eps):
+    """RMS normalisation over the last axis (every head of a token): statistics in fp32, the
+    normalised row rounded to x's dtype, then scaled by `weight` in that dtype (the
+    reference's _tp_rms / _tp_rms_qk, models/fast_dit.py:134-160, whose all-reduce is the
+    identity at TP=1)."""
     xf = x.float()
-    ss = xf.pow(2).sum(-1, keepdim=True)
-    return (xf * torch.rsqrt(ss / x.shape[-1] + norm.eps)).type_as(x) * norm.weight
+    mean_sq = torch.sum(xf * xf, dim=-1, keepdim=True) / x.shape[-1]
+    return (xf * torch.rsqrt(mean_sq + eps)).to(x.dtype) * weight
 
 
 def _rope(x, cos, sin):
-    """x [B, L, n, d]; cos/sin [L, d/2] fp32: interleaved-pair rotation in fp32."""
-    B, L, n, d = x.shape
-    c = cos.view(1, L, 1, d // 2)
-    s = sin.view(1, L, 1, d // 2)
-    xp = x.float().reshape(B, L, n, d // 2, 2)
-    xr, xi = xp[..., 0], xp[..., 1]
-    out = torch.stack([xr * c - xi * s, xr * s + xi * c], dim=-1)
-    return out.reshape(B, L, n, d).to(x.dtype)
+    """3D-RoPE of x [B, L, H, D]: channel pair (2j, 2j+1) of token l is turned by the angle
+    whose cosine and sine are cos[l, j], sin[l, j] (fp32 tables [L, D/2]); fp32 arithmetic,
+    one rounding back to x's dtype (models/fast_dit.py:163-169)."""
+    pairs = x.float().unflatten(-1, (-1, 2))
+    re, im = pairs[..., 0], pairs[..., 1]
+    c, s = cos[:, None, :], sin[:, None, :]          # broadcast over batch and heads
+    return torch.stack((re * c - im * s, re * s + im * c), dim=-1).flatten(-2).to(x.dtype)
 
 
-def _modulate(x, shift, scale, num_frames):
-    """x [B, L, C]; shift/scale [1, F, C] broadcast over each frame's tokens."""
-    B, L, C = x.shape
-    xv = x.view(B, num_frames, L // num_frames, C)
-    return (xv * (1 + scale.unsqueeze(2)) + shift.unsqueeze(2)).view(B, L, C)
+def _by_frame(t, num_frames):
+    """[B, L, C] -> [B, F, L/F, C]: each latent frame's tokens are contiguous."""
+    return t.unflatten(1, (num_frames, t.shape[1] // num_frames))
 
 
-def _gate(y, gate, num_frames):
-    B, L, C = y.shape
-    return (y.view(B, num_frames, L // num_frames, C) * gate.unsqueeze(2)).view(B, L, C)
+def _eager_stage(x, y, e, num_frames, gate=-1, shift=-1, scale=-1, ln=None, norm=True):
+    """One pointwise stage as separate torch ops (models/fast_dit.py:172-181,280,294,306-311);
+    the same contract as ops.adaln.  e: [F, n, C] rows; returns (r, h):
+        r = x, x + y, or x + y * e[gate]            (product and sum each rounded)
+        h = ln(r), then h * (1 + e[scale]) + e[shift] per frame   (None when norm is False)"""
+    def row(i):
+        return e[:, i].unsqueeze(1)                  # [F, 1, C] against [B, F, L/F, C]
+    r = x
+    if y is not None:
+        if gate >= 0:
+            y = (_by_frame(y, num_frames) * row(gate)).flatten(1, 2)
+        r = x + y
+    if not norm:
+        return r, None
+    h = ln(r)
+    if shift >= 0:
+        h = (_by_frame(h, num_frames) * (1 + row(scale)) + row(shift)).flatten(1, 2)
+    return r, h
 
 
-# ─── attention backends: q [B, Lq, n, d], k/v [B, Lk, n, d] -> [B, Lq, n, d] ───
+def _hip_stage(x, y, e, num_frames, gate=-1, shift=-1, scale=-1, ln=None, norm=True):
+    """The same stage as one fused pass over the residual stream (wan_adaln)."""
+    w = b = None
+    if ln is not None and ln.weight is not None:
+        w, b = ln.weight, ln.bias
+    eps = ln.eps if ln is not None else 1e-6
+    return ops.adaln(x, y, e, num_frames, gate_idx=gate, shift_idx=shift, scale_idx=scale,
+                     ln_weight=w, ln_bias=b, eps=eps, norm=norm)
+
+
+def _ffn_eager(h, ffn):
+    return _linear(ffn[1](_linear(h, ffn[0])), ffn[2])
+
+
+def _ffn_gelu_epilogue(h, ffn):
+    """FFN with the tanh-GELU applied in the first GEMM's epilogue (hipBLASLt)."""
+    B, L, C = h.shape
+    up = torch._addmm_activation(ffn[0].bias, h.reshape(B * L, C), ffn[0].weight.t(), use_gelu=True)
+    return _linear(up.view(B, L, -1), ffn[2])
+
+
+# ─── attention backends: q [B, Lq, n, d], k/v [B, Lk, n, d] -> [B, Lq, n, d] ───────
 
 def _sdpa(q, k, v, seqlen_k: Optional[Sequence[int]] = None, scale: Optional[float] = None):
-    """torch SDPA over [B, L, n, d] views.  On a HIP device it runs in fp32 on contiguous
-    [B, n, L, d] copies (torch's bf16 batched products over transposed views are not used)."""
+    """torch SDPA over [B, L, n, d] views (the reference's _sdpa, models/fast_dit.py:186-189).
+    On a HIP device it runs in fp32 on contiguous [B, n, L, d] copies (torch's bf16 batched
+    products over transposed views are not used).  seqlen_k: keys per sample."""
     def one(qb, kb, vb):
         qt, kt, vt = (t.transpose(1, 2) for t in (qb, kb, vb))
         if qt.device.type == "cuda":
@@ -109,27 +137,9 @@ def _sdpa(q, k, v, seqlen_k: Optional[Sequence[int]] = None, scale: Optional[flo
     return torch.cat([one(q[b:b + 1], k[b:b + 1, :n], v[b:b + 1, :n]) for b, n in enumerate(seqlen_k)], 0)
 
 
-def _hip_self(q, k, v):
-    return ops.flash_self_attn(q, k, v, q.shape[-1] ** -0.5, 0)
-
-
-def _hip_cross(q, k, v, seqlen_k: Optional[torch.Tensor] = None):
-    return ops.cross_attn(q, k, v, seqlen_k, q.shape[-1] ** -0.5)
-
-
-def _hip_self_fused(q, k, v, norm_q, norm_k, cos, sin):
-    return ops.self_attn_fused(q, k, v, norm_q.weight, norm_k.weight, norm_q.eps, cos, sin,
-                               q.shape[-1] ** -0.5)
-
-
-def _hip_cross_fused(q, k, v, norm_q, seqlen_k: Optional[torch.Tensor] = None):
-    return ops.cross_attn_fused(q, k, v, norm_q.weight, norm_q.eps, seqlen_k, q.shape[-1] ** -0.5)
-
-
-# ─── compiled-unit equivalents ────────────────────────────────────────────────
-
 class _FastBlock:
-    """One WanAttentionBlock forward (models/fast_dit.py:260-311) at TP=1."""
+    """One WanAttentionBlock forward (the reference's _FastBlock, models/fast_dit.py:260-311)
+    at TP=1, as the four stages of the module docstring."""
 
     def __init__(self, block, num_frames: int, attn_impl: str = FAST_ATTN_IMPL,
                  cross_impl: str = FAST_CROSS_IMPL, pointwise_impl: str = FAST_POINTWISE_IMPL):
@@ -144,160 +154,135 @@ class _FastBlock:
             self.b_qkv = torch.cat([sa.q.bias, sa.k.bias, sa.v.bias], 0).contiguous()
 
     def __call__(self, x, e0, cos, sin, ck, cv, seqlen_k=None):
+        """x [B, L, C] bf16; e0 [1, F, 6, C] time projection; cos/sin [L, 64]; ck/cv the
+        block's text keys/values [B, Lc, n, d]; seqlen_k: per-sample text lengths or None."""
         blk, nf = self.block, self.num_frames
-        sa, ca = blk.self_attn, blk.cross_attn
         B, L, C = x.shape
+        fused = self.pointwise_impl == "hip" and x.is_cuda
+        stage = _hip_stage if fused else _eager_stage
+        e = (blk.modulation.unsqueeze(0) + e0).reshape(nf, 6, C)
+        if fused:
+            x = x.contiguous()
+        _, h = stage(x, None, e, nf, shift=0, scale=1, ln=blk.norm1)
+        y = _linear(self._self_attention(h, cos, sin).reshape(B, L, C), blk.self_attn.o)
+        x, h = stage(x, y, e, nf, gate=2, ln=blk.norm3)
+        y = _linear(self._cross_attention(h, ck, cv, seqlen_k).reshape(B, L, C), blk.cross_attn.o)
+        x, h = stage(x, y, e, nf, shift=3, scale=4, ln=blk.norm2)
+        y = (_ffn_gelu_epilogue if fused else _ffn_eager)(h, blk.ffn)
+        x, _ = stage(x, y, e, nf, gate=5, norm=False)
+        return x
 
-        if self.pointwise_impl == "hip" and x.is_cuda:
-            return self._fused(x, e0, cos, sin, ck, cv, seqlen_k)
-        e = (blk.modulation.unsqueeze(0) + e0).chunk(6, dim=2)
-        e = [t.squeeze(2) for t in e]  # each [1, F, C]
-
-        # self-attention
-        h = _modulate(blk.norm1(x).to(torch.bfloat16), e[0], e[1], nf)
-        y = _lin(self._self_attn(h, cos, sin).reshape(B, L, C), sa.o)
-        x = x + _gate(y, e[2], nf)
-
-        # cross-attention; ck/cv [B, Lc, n, d] precomputed once per prompt (_FastCrossKV)
-        h = blk.norm3(x)
-        x = x + _lin(self._cross_attn(h, ck, cv, seqlen_k).reshape(B, L, C), ca.o)
-
-        # FFN
-        h = _modulate(blk.norm2(x).to(torch.bfloat16), e[3], e[4], nf)
-        h = blk.ffn[1](_lin(h, blk.ffn[0]))
-        y = _lin(h, blk.ffn[2])
-        return x + _gate(y, e[5], nf)
-
-    def _self_attn(self, h, cos, sin):
-        blk = self.block
-        sa = blk.self_attn
+    def _self_attention(self, h, cos, sin):
+        sa = self.block.self_attn
         B, L, C = h.shape
-        n, d = sa.num_heads, sa.head_dim
+        heads = (B, L, sa.num_heads, sa.head_dim)
+        scale = sa.head_dim ** -0.5
         if self.attn_impl == "hip":
-            qkv = F.linear(h, self.w_qkv, self.b_qkv)
-            q, k, v = (qkv[..., i * C:(i + 1) * C].view(B, L, n, d) for i in range(3))
-            return _hip_self_fused(q, k, v, sa.norm_q, sa.norm_k, cos, sin)
-        q, k = _tp_rms_qk(_lin(h, sa.q), _lin(h, sa.k), sa.norm_q, sa.norm_k)
-        v = _lin(h, sa.v).view(B, L, n, d)
-        return _sdpa(_rope(q.view(B, L, n, d), cos, sin), _rope(k.view(B, L, n, d), cos, sin), v)
+            q, k, v = (t.view(heads) for t in F.linear(h, self.w_qkv, self.b_qkv).split(C, dim=-1))
+            return ops.self_attn_fused(q, k, v, sa.norm_q.weight, sa.norm_k.weight, sa.norm_q.eps,
+                                       cos, sin, scale)
+        q = _rms_normalize(_linear(h, sa.q), sa.norm_q.weight, sa.norm_q.eps).view(heads)
+        k = _rms_normalize(_linear(h, sa.k), sa.norm_k.weight, sa.norm_k.eps).view(heads)
+        return _sdpa(_rope(q, cos, sin), _rope(k, cos, sin), _linear(h, sa.v).view(heads))
 
-    def _cross_attn(self, h, ck, cv, seqlen_k):
+    def _cross_attention(self, h, ck, cv, seqlen_k):
         ca = self.block.cross_attn
         B, L, C = h.shape
-        n, d = ca.num_heads, ca.head_dim
+        heads = (B, L, ca.num_heads, ca.head_dim)
+        q = _linear(h, ca.q)
         if self.cross_impl == "hip":
-            return _hip_cross_fused(_lin(h, ca.q).view(B, L, n, d), ck, cv, ca.norm_q, seqlen_k)
-        q = _tp_rms(_lin(h, ca.q), ca.norm_q).view(B, L, n, d)
+            return ops.cross_attn_fused(q.view(heads), ck, cv, ca.norm_q.weight, ca.norm_q.eps,
+                                        seqlen_k, ca.head_dim ** -0.5)
+        q = _rms_normalize(q, ca.norm_q.weight, ca.norm_q.eps).view(heads)
         return _sdpa(q, ck, cv, None if seqlen_k is None else seqlen_k.tolist())
 
-    def _fused(self, x, e0, cos, sin, ck, cv, seqlen_k):
-        """The same block with its pointwise chain in four fused adaLN passes
-        (models/fast_dit.py:280, :294, :306-307, :311) and GELU in the FFN-up GEMM."""
-        blk, nf = self.block, self.num_frames
-        B, L, C = x.shape
-        e = (blk.modulation.unsqueeze(0) + e0).reshape(nf, 6, C)      # rows 0..5 per frame
-        x = x.contiguous()
-        _, h = ops.adaln(x, e=e, frames=nf, shift_idx=0, scale_idx=1, eps=blk.norm1.eps)
-        y = _lin(self._self_attn(h, cos, sin).reshape(B, L, C), blk.self_attn.o)
-        x, h = ops.adaln(x, y, e, nf, gate_idx=2, ln_weight=blk.norm3.weight,
-                         ln_bias=blk.norm3.bias, eps=blk.norm3.eps)
-        y = _lin(self._cross_attn(h, ck, cv, seqlen_k).reshape(B, L, C), blk.cross_attn.o)
-        x, h = ops.adaln(x, y, e, nf, shift_idx=3, scale_idx=4, eps=blk.norm2.eps)
-        f0, f2 = blk.ffn[0], blk.ffn[2]
-        h = torch._addmm_activation(f0.bias, h.view(B * L, C), f0.weight.t(), use_gelu=True)
-        y = _lin(h.view(B, L, -1), f2)
-        x, _ = ops.adaln(x, y, e, nf, gate_idx=5, norm=False)
-        return x
+
+def cross_kv(block, context, impl: str = FAST_CROSS_IMPL):
+    """The text keys and values one block attends to, [B, Lc, n, d] each: K RMS-normalised
+    over all heads of a text token, V as projected.  Computed once per prompt and kept in
+    HBM for every denoising step (the reference's _FastCrossKV, models/fast_dit.py:464-477)."""
+    ca = block.cross_attn
+    B, Lc, _ = context.shape
+    heads = (B, Lc, ca.num_heads, ca.head_dim)
+    k = _linear(context, ca.k)
+    if impl == "hip":
+        k = ops.rms_norm(k.view(heads), ca.norm_k.weight, ca.norm_k.eps)
+    else:
+        k = _rms_normalize(k, ca.norm_k.weight, ca.norm_k.eps).view(heads)
+    return k, _linear(context, ca.v).view(heads)
 
 
 class _FastCrossKV:
-    """A block's cross-attention K (normalised) and V from the text context, once per prompt."""
+    """cross_kv() bound to one block (the reference's per-block callable)."""
 
     def __init__(self, block, cross_impl: str = FAST_CROSS_IMPL):
-        self.block = block
-        self.cross_impl = cross_impl
+        self.block, self.cross_impl = block, cross_impl
 
     def __call__(self, context):
-        ca = self.block.cross_attn
-        B, Lc, _ = context.shape
-        n, d = ca.num_heads, ca.head_dim
-        k = _lin(context, ca.k).view(B, Lc, n, d)
-        if self.cross_impl == "hip":
-            k = ops.rms_norm(k, ca.norm_k.weight, ca.norm_k.eps)
-        else:
-            k = _tp_rms(k.reshape(B, Lc, n * d), ca.norm_k).view(B, Lc, n, d)
-        v = _lin(context, ca.v).view(B, Lc, n, d)
-        return k, v
+        return cross_kv(self.block, context, self.cross_impl)
 
 
-class _FastHead:
-    """Head + unpatchify + CFG combine -> [C_out, F, H, W] (batch is [cond, uncond])."""
-
-    def __init__(self, head, grid, patch_size, out_dim, guide_scale):
-        self.head = head
-        self.grid = grid
-        self.patch_size = patch_size
-        self.out_dim = out_dim
-        self.guide_scale = guide_scale
-
-    def __call__(self, x, e):
-        hd = self.head
-        f, h, w = self.grid
-        p, q, r = self.patch_size
-        c = self.out_dim
-        m = (hd.modulation.unsqueeze(0) + e.unsqueeze(2)).chunk(2, dim=2)
-        y = hd.head(_modulate(hd.norm(x), m[0].squeeze(2), m[1].squeeze(2), f))
-        B = y.shape[0]
-        y = y.view(B, f, h, w, p, q, r, c).permute(0, 7, 1, 4, 2, 5, 3, 6)
-        y = y.reshape(B, c, f * p, h * q, w * r).to(torch.bfloat16)
-        cond, uncond = y[0], y[1]
-        return uncond + self.guide_scale * (cond - uncond)
+def noise_prediction(head, x, e, grid, patch_size, out_dim, guide_scale):
+    """Output head and CFG (the reference's _FastHead, models/fast_dit.py:480-505): the final
+    tokens x [2, L, C] get the head's per-frame adaLN (modulation rows from the time
+    embedding e [1, F, C]) and its projection to one patch of out_dim channels each; the
+    patches go back to the latent grid [2, out_dim, F*pt, H*ph, W*pw]; batch row 0 is the
+    cond and row 1 the uncond prediction, returned as uncond + guide (cond - uncond)."""
+    f, hh, ww = grid
+    pt, ph, pw = patch_size
+    C = x.shape[-1]
+    rows = (head.modulation.unsqueeze(0) + e.unsqueeze(2)).reshape(f, 2, C)   # shift, scale
+    _, h = _eager_stage(x, None, rows, f, shift=0, scale=1, ln=head.norm)
+    y = _linear(h, head.head)
+    n = y.shape[0]
+    # token (t, i, j) patch (a, b, c) channel o -> latent [o, t*pt + a, i*ph + b, j*pw + c]
+    y = y.view(n, f, hh, ww, pt, ph, pw, out_dim).permute(0, 7, 1, 4, 2, 5, 3, 6)
+    y = y.reshape(n, out_dim, f * pt, hh * ph, ww * pw).to(torch.bfloat16)
+    cond, uncond = y[0], y[1]
+    return uncond + guide_scale * (cond - uncond)
 
 
 class FastWanDiT:
-    """Batched-CFG forward over a WanModel (models/fast_dit.py:561-697).
-
-        fast = FastWanDiT(model, grid=(F, H/2, W/2), guide_scale=5.0)
-        fast.set_context(ctx_cond, ctx_null)   # [1, 512, 4096] each, once per prompt
-        noise_pred = fast(latent, t)           # latent [C, F, H, W], t scalar
-    """
+    """The whole DiT with batched CFG on one GPU (the reference's FastWanDiT,
+    models/fast_dit.py:561-697).  Per prompt, set_context() embeds the two text contexts and
+    precomputes every block's text K/V; per denoising step, calling the object with the
+    latent [C, F, H, W] and the timestep returns the guided flow prediction [C, F, H, W]."""
 
     def __init__(self, model: WanModel, grid, guide_scale: float, attn_impl: str = FAST_ATTN_IMPL,
                  cross_impl: str = FAST_CROSS_IMPL, pointwise_impl: str = FAST_POINTWISE_IMPL):
         self.model = model
         self.grid = tuple(int(g) for g in grid)
         self.num_frames = self.grid[0]
-        self.seq_len = self.grid[0] * self.grid[1] * self.grid[2]
-        dev = model.patch_embedding.weight.device
-        self.device = dev
+        self.seq_len = math.prod(self.grid)
+        self.guide_scale = guide_scale
+        self.device = model.patch_embedding.weight.device
         head_dim = model.dim // model.num_heads
-        self.cos, self.sin = _rope_mod.rope_tables(model.freqs, self.grid, head_dim, dev)
+        self.cos, self.sin = _rope_mod.rope_tables(model.freqs, self.grid, head_dim, self.device)
         self.blocks = [_FastBlock(b, self.num_frames, attn_impl, cross_impl, pointwise_impl)
                        for b in model.blocks]
-        self.cross_kv = [_FastCrossKV(b, cross_impl) for b in model.blocks]
-        self.head = _FastHead(model.head, self.grid, model.patch_size, model.out_dim, guide_scale)
+        self.cross_impl = cross_impl
         self.context = None
         self.seqlen_k = None
 
     def set_context(self, ctx_cond, ctx_null, context_lens: Optional[Sequence[int]] = None):
-        """Text embedding and every block's cross K/V, once per prompt.  context_lens: the
-        number of valid text tokens of (cond, uncond); None attends to all 512 tokens as the
-        reference pipeline does."""
+        """ctx_cond / ctx_null [1, Lc, text_dim]: the text embedding and every block's cross
+        K/V, once per prompt.  context_lens: valid text tokens of (cond, uncond); None attends
+        to all Lc tokens, as the reference pipeline does."""
         ctx = torch.cat([ctx_cond, ctx_null], dim=0).to(self.device, torch.bfloat16)
-        context = self.model.text_embedding(ctx)
-        self.context = [kv(context) for kv in self.cross_kv]
+        text = self.model.text_embedding(ctx)
+        self.context = [cross_kv(b, text, self.cross_impl) for b in self.model.blocks]
         self.seqlen_k = None if context_lens is None else \
             torch.tensor(list(context_lens), dtype=torch.int32, device=self.device)
 
-    def _time_embed(self, t):
-        """Per-frame time embedding: frame 0 (the conditioning image) has t=0, the rest t."""
+    def time_rows(self, t):
+        """Time conditioning per latent frame.  Frame 0 holds the conditioning image and is
+        embedded at t = 0, the others at t.  Returns the head's embedding [1, F, C] and the
+        blocks' modulation input [1, F, 6, C]."""
         m = self.model
-        t_frames = torch.full((self.num_frames,), float(t), dtype=torch.float64)
-        t_frames[0] = 0.0
-        s = sinusoidal_embedding_1d(m.freq_dim, t_frames).to(torch.bfloat16).to(self.device).unsqueeze(0)
-        e = m.time_embedding(s)                                # [1, F, C]
-        e0 = m.time_projection(e).unflatten(2, (6, m.dim))     # [1, F, 6, C]
-        return e, e0
+        frame_t = float(t) * (torch.arange(self.num_frames) > 0).double()
+        sincos = sinusoidal_embedding_1d(m.freq_dim, frame_t).to(torch.bfloat16).to(self.device)
+        emb = m.time_embedding(sincos.unsqueeze(0))
+        return emb, m.time_projection(emb).view(1, self.num_frames, 6, m.dim)
 
     def patch(self, latent):
         """Patch embedding (a Conv3d with stride = kernel = patch_size) as one GEMM: gather
@@ -312,28 +297,32 @@ class FastWanDiT:
         return x.unsqueeze(0).expand(2, -1, -1).contiguous()
 
     def __call__(self, latent, t):
-        assert self.context is not None, "call set_context() first"
-        e, e0 = self._time_embed(t)
+        if self.context is None:
+            raise RuntimeError("FastWanDiT: call set_context() before the first step")
+        e, e0 = self.time_rows(t)
         x = self.patch(latent)
         for blk, (ck, cv) in zip(self.blocks, self.context):
             x = blk(x, e0, self.cos, self.sin, ck, cv, self.seqlen_k)
-        return self.head(x, e)
+        m = self.model
+        return noise_prediction(m.head, x, e, self.grid, m.patch_size, m.out_dim, self.guide_scale)
 
 
 def denoise(fast: FastWanDiT, latent: torch.Tensor, steps: int, shift: float,
             image_latent: Optional[torch.Tensor] = None, num_train_timesteps: int = 1000):
-    """The TI2V denoising loop (inference_neuron_ti2v.py:450-531): UniPC over `steps`
-    timesteps with the scheduler step on the device; if `image_latent` [C, 1, H, W] is
-    given, frame 0 is reset to it after every step (the mask2 blend)."""
+    """The TI2V denoising loop (inference_neuron_ti2v.py:448-531): the latent in bf16 as the
+    reference keeps it, one DiT call and one UniPC step (on the device) per timestep; with
+    `image_latent` [C, 1, H, W], frame 0 is the image latent before the first call and after
+    every step (the mask2 blend).  Returns the final bf16 latent."""
     from .unipc import FlowUniPC
-    sched = FlowUniPC(num_train_timesteps=num_train_timesteps, shift=1.0)
-    sched.set_timesteps(steps, shift=shift)
-    if image_latent is not None:
-        latent = latent.clone()
-        latent[:, :1] = image_latent
-    for t in sched.timesteps:
-        noise_pred = fast(latent, t)
-        latent = sched.step(noise_pred, latent)
-        if image_latent is not None:
-            latent[:, :1] = image_latent
-    return latent
+    sampler = FlowUniPC(num_train_timesteps=num_train_timesteps, shift=1.0)
+    sampler.set_timesteps(steps, shift=shift)
+    x = latent.to(torch.bfloat16)
+    image = None if image_latent is None else image_latent.to(x.device, torch.bfloat16)
+    if image is not None:
+        x = x.clone()
+        x[:, :1] = image
+    for t in sampler.timesteps:
+        x = sampler.step(fast(x, t), x)
+        if image is not None:
+            x[:, :1] = image
+    return x
