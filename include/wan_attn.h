@@ -108,6 +108,24 @@ int wan_cross_attn_fused(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor ou
                          void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * wan_cross_attn_fused without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the reference.  The per-row inverse RMS of q goes
+ * to a scratch array owned by the library: WAN_NOALLOC_MAX_ROWS fp32 rows (512 KB) per
+ * GPU, held until the process ends; batch * seqlen_q above that returns
+ * WAN_ERR_UNSUPPORTED.  The array's device address is looked up on the first call on
+ * each device (the device current at the call).  Nothing is allocated or freed.  Every
+ * call on one GPU shares that GPU's array: calls that overlap on one GPU (e.g. on two
+ * streams) race and must be ordered by the caller.  Same kernels and results as
+ * wan_cross_attn_fused.
+ */
+#define WAN_NOALLOC_MAX_ROWS (1 << 17)
+int wan_cross_attn_fused_noalloc(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor out,
+                                 int batch, int heads, int seqlen_q, int seqlen_k, int head_dim,
+                                 const void* gamma_q, float eps, float softmax_scale,
+                                 const int32_t* seqlen_k_dev, void* stream);
+
+/*
  * 3D-RoPE interleaved-pair rotation in fp32 with one bf16 rounding:
  * out [B, L, H, 128] contiguous.  Semantics of _rope, models/fast_dit.py:163-169
  * (the named kernel causal_rope_rotation, kernels/rope.py:39-71, computes the

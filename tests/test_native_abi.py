@@ -180,3 +180,15 @@ def test_softmax_scale_must_be_finite_and_positive(W, scale):
     for name, call in calls.items():
         assert call() == 2, name
         assert "softmax_scale" in N.last_error() and name in N.last_error()
+
+
+def test_noalloc_rejects_rows_beyond_its_scratch(W):
+    """wan_cross_attn_fused_noalloc's static scratch holds WAN_NOALLOC_MAX_ROWS query rows;
+    a larger batch * seqlen_q is refused before any device call."""
+    N = W._native
+    lib = N.lib()
+    t = N.WanTensor(64, 24 * 128 * 16, 24 * 128, 128)
+    rc = lib.wan_cross_attn_fused_noalloc(t, t, t, t, 16, 24, 8193, 16, 128, 256, 1e-6, 0.088, None, None)
+    assert rc == 2 and "static scratch" in N.last_error()
+    rc = lib.wan_cross_attn_fused_noalloc(t, t, t, t, 1, 24, 16, 16, 128, 256, 1e-6, 0.0, None, None)
+    assert rc == 2 and "softmax_scale" in N.last_error()

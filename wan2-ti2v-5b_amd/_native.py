@@ -41,6 +41,7 @@ SIGNATURES = {
     "wan_self_attn_fused": (_I, [_T, _T, _T, _T, _I, _I, _I, _I, _P, _P, _F, _P, _P, _F, _P, _SZ, _P]),
     "wan_cross_attn_fused_workspace": (_SZ, [_I, _I, _I]),
     "wan_cross_attn_fused": (_I, [_T, _T, _T, _T, _I, _I, _I, _I, _I, _P, _F, _F, _P, _P, _SZ, _P]),
+    "wan_cross_attn_fused_noalloc": (_I, [_T, _T, _T, _T, _I, _I, _I, _I, _I, _P, _F, _F, _P, _P]),
     "wan_rope": (_I, [_T, _P, _I, _I, _I, _I, _P, _P, _P]),
     "wan_rms_norm": (_I, [_T, _P, _I, _I, _I, _I, _P, _F, _P, _P, _P, _P]),
     "wan_rms_norm_qk": (_I, [_T, _T, _P, _I, _I, _I, _I, _P, _F, _P, _P, _P, _P]),

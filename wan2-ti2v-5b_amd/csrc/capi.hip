@@ -6,6 +6,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "../../include/wan_attn.h"
 #include "common.h"
 
@@ -295,11 +297,24 @@ size_t wan_cross_attn_fused_workspace(int batch, int heads, int seqlen_q) {
   return align_up((size_t)batch * seqlen_q * sizeof(float));
 }
 
-int wan_cross_attn_fused(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor out, int batch,
-                         int heads, int seqlen_q, int seqlen_k, int head_dim, const void* gamma_q,
-                         float eps, float softmax_scale, const int32_t* seqlen_k_dev,
-                         void* workspace, size_t workspace_bytes, void* stream) {
-  const char* fn = "wan_cross_attn_fused";
+}  // extern "C"
+
+namespace wan {
+// Library-owned scratch of wan_cross_attn_fused_noalloc: the fp32 inverse RMS of each
+// query row, WAN_NOALLOC_MAX_ROWS rows (512 KB) per GPU, held until the process ends.
+// In host code `scratch` names a host-side stand-in, not device memory: its device
+// address is looked up once per device with hipGetSymbolAddress (that device current)
+// and only that address is handed to the kernels.
+__device__ __align__(256) float scratch[WAN_NOALLOC_MAX_ROWS];
+}  // namespace wan
+
+namespace {
+
+// Validation shared by the two fused cross-attention entry points (everything but the
+// workspace).  Returns WAN_OK, or an error code with the message set.
+int check_cross_fused(const char* fn, const wan_tensor& q, const wan_tensor& k, const wan_tensor& v,
+                      const wan_tensor& out, int batch, int heads, int seqlen_q, int seqlen_k,
+                      int head_dim, const void* gamma_q, float eps, float softmax_scale) {
   int rc;
   if ((rc = check_scale(fn, softmax_scale))) return rc;
   if ((rc = check_dims(fn, batch, heads, seqlen_q, seqlen_k, head_dim))) return rc;
@@ -311,18 +326,87 @@ int wan_cross_attn_fused(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor ou
   if (!gamma_q || !aligned16(gamma_q))
     return set_error(WAN_ERR_INVALID, "%s: gamma_q must be a 16-byte aligned pointer", fn);
   if (!(eps >= 0.f)) return set_error(WAN_ERR_INVALID, "%s: eps must be >= 0", fn);
+  return WAN_OK;
+}
+
+// The two launches of a fused cross-attention, with the per-row inverse RMS of q in inv_q.
+int cross_fused_launch(const wan_tensor& q, const wan_tensor& k, const wan_tensor& v,
+                       const wan_tensor& out, int batch, int heads, int seqlen_q, int seqlen_k,
+                       int head_dim, const void* gamma_q, float eps, float softmax_scale,
+                       const int32_t* seqlen_k_dev, float* inv_q, void* stream) {
+  int rc;
+  if ((rc = wan_rms_norm(q, nullptr, batch, seqlen_q, heads, head_dim, nullptr, eps, nullptr,
+                         nullptr, inv_q, stream)))
+    return rc;
+  return wan_flash_attn_qnorm(q, k, v, out, batch, heads, seqlen_q, seqlen_k, head_dim, inv_q,
+                              gamma_q, nullptr, nullptr, softmax_scale, seqlen_k_dev, stream);
+}
+
+constexpr int kMaxDevices = 64;
+float* g_scratch_dev[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+
+// The current device's copy of `scratch` (looked up on the first call on that device).
+int device_scratch(const char* fn, float** ptr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(WAN_ERR_LAUNCH, "%s: hipGetDevice: %s", fn, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return set_error(WAN_ERR_UNSUPPORTED, "%s: device %d beyond the %d devices supported", fn, dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return set_error(WAN_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch) on device %d: %s", fn, dev,
+                       hipGetErrorString(e));
+    g_scratch_dev[dev] = static_cast<float*>(p);
+  }
+  *ptr = g_scratch_dev[dev];
+  return WAN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int wan_cross_attn_fused(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor out, int batch,
+                         int heads, int seqlen_q, int seqlen_k, int head_dim, const void* gamma_q,
+                         float eps, float softmax_scale, const int32_t* seqlen_k_dev,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "wan_cross_attn_fused";
+  int rc;
+  if ((rc = check_cross_fused(fn, q, k, v, out, batch, heads, seqlen_q, seqlen_k, head_dim,
+                              gamma_q, eps, softmax_scale)))
+    return rc;
+  if (batch == 0 || heads == 0 || seqlen_q == 0) return WAN_OK;
   const size_t need = wan_cross_attn_fused_workspace(batch, heads, seqlen_q);
   if (workspace == nullptr || workspace_bytes < need)
     return set_error(WAN_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, %zu given", fn, need,
                      workspace ? workspace_bytes : (size_t)0);
   if (reinterpret_cast<uintptr_t>(workspace) % kAlign)
     return set_error(WAN_ERR_INVALID, "%s: workspace must be 256-byte aligned", fn);
-  float* inv_q = static_cast<float*>(workspace);
-  if ((rc = wan_rms_norm(q, nullptr, batch, seqlen_q, heads, head_dim, nullptr, eps, nullptr,
-                         nullptr, inv_q, stream)))
+  return cross_fused_launch(q, k, v, out, batch, heads, seqlen_q, seqlen_k, head_dim, gamma_q, eps,
+                            softmax_scale, seqlen_k_dev, static_cast<float*>(workspace), stream);
+}
+
+int wan_cross_attn_fused_noalloc(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor out,
+                                 int batch, int heads, int seqlen_q, int seqlen_k, int head_dim,
+                                 const void* gamma_q, float eps, float softmax_scale,
+                                 const int32_t* seqlen_k_dev, void* stream) {
+  const char* fn = "wan_cross_attn_fused_noalloc";
+  int rc;
+  if ((rc = check_cross_fused(fn, q, k, v, out, batch, heads, seqlen_q, seqlen_k, head_dim,
+                              gamma_q, eps, softmax_scale)))
     return rc;
-  return wan_flash_attn_qnorm(q, k, v, out, batch, heads, seqlen_q, seqlen_k, head_dim, inv_q,
-                              gamma_q, nullptr, nullptr, softmax_scale, seqlen_k_dev, stream);
+  if ((int64_t)batch * seqlen_q > (int64_t)WAN_NOALLOC_MAX_ROWS)
+    return set_error(WAN_ERR_UNSUPPORTED, "%s: batch*seqlen_q=%lld exceeds the static scratch of %d rows",
+                     fn, (long long)batch * seqlen_q, WAN_NOALLOC_MAX_ROWS);
+  if (batch == 0 || heads == 0 || seqlen_q == 0) return WAN_OK;
+  float* inv_q = nullptr;
+  if ((rc = device_scratch(fn, &inv_q))) return rc;
+  return cross_fused_launch(q, k, v, out, batch, heads, seqlen_q, seqlen_k, head_dim, gamma_q, eps,
+                            softmax_scale, seqlen_k_dev, inv_q, stream);
 }
 
 int wan_rope(wan_tensor x, void* out, int batch, int seqlen, int heads, int head_dim,
