@@ -331,6 +331,52 @@ def test_cross_config_b(W, lens):
     assert ref.rel_rms(out, want) <= 5e-3
 
 
+@pytest.mark.parametrize("fused", [False, True])
+def test_persistent_cross_mixed_lengths(W, fused):
+    """Per-sample key lengths select the persistent short-key kernel: each workgroup walks
+    several (batch, head, 128-row block) items, fetching the next item's tiles and query
+    rows while it finishes the current one.  Five samples with lengths 512, 0, 1, 130 and
+    64 (full, empty, a single key, partial and exactly one tile), NaN and huge K past each
+    length, 24 heads: many items per workgroup, in every order of long and short."""
+    B, H, Lq, Lk = 5, 24, 1000, 512
+    lens = [512, 0, 1, 130, 64]
+    q, ck, cv = _bf((B, Lq, H, D), 401), _bf((B, Lk, H, D), 402), _bf((B, Lk, H, D), 403)
+    gq = _gammas(H * D, 404, True)
+    ck2, cv2 = ck.clone(), cv.clone()
+    for b, n in enumerate(lens):
+        ck2[b, n:] = _bf((Lk - n, H, D), 410 + b, std=50.0)
+        cv2[b, n:] = float("nan")
+    sk = torch.tensor(lens, dtype=torch.int32).to(DEV)
+    if fused:
+        out = W.ops.cross_attn_fused(*_d(q, ck2, cv2, gq), 1e-6, sk, SCALE).cpu()
+        qn = ref.rms(q.reshape(B, Lq, H * D), gq).view(B, Lq, H, D)
+    else:
+        out = W.ops.cross_attn(*_d(q, ck2, cv2), sk, SCALE).cpu()
+        qn = q
+    assert torch.isfinite(out.float()).all()
+    assert torch.count_nonzero(out[1]) == 0
+    want = ref.sdpa(qn.float(), ck.float(), cv.float(), seqlen_k=lens)
+    for b in (0, 2, 3, 4):
+        e = ref.rel_rms(out[b], want[b])
+        print(f"fused={fused} len={lens[b]}: rel_rms vs fp32 {e:.3e}")
+        assert e <= 5e-3
+
+
+@pytest.mark.parametrize("B,Lq,Lk", [(2, 7854, 512), (3, 130, 77), (1, 5, 64)])
+def test_persistent_equals_plain_kernel(W, B, Lq, Lk):
+    """Lengths all equal to Lk (the persistent kernel) against no lengths (the plain
+    short-key kernel): the same arithmetic in the same order, so the same bits; the
+    small shapes have fewer items than workgroups."""
+    H = 24 if Lq > 1000 else 3
+    q, ck, cv = _bf((B, Lq, H, D), 501), _bf((B, Lk, H, D), 502), _bf((B, Lk, H, D), 503)
+    gq = _gammas(H * D, 504, True)
+    sk = torch.full((B,), Lk, dtype=torch.int32).to(DEV)
+    qd, kd, vd, gd = _d(q, ck, cv, gq)
+    assert torch.equal(W.ops.cross_attn_fused(qd, kd, vd, gd, 1e-6, sk, SCALE),
+                       W.ops.cross_attn_fused(qd, kd, vd, gd, 1e-6, None, SCALE))
+    assert torch.equal(W.ops.cross_attn(qd, kd, vd, sk, SCALE), W.ops.cross_attn(qd, kd, vd, None, SCALE))
+
+
 def test_cross_masked_keys_do_not_matter(W):
     B, H, Lq, Lk = 2, 24, 1000, 512
     q, ck, cv = _bf((B, Lq, H, D), 61), _bf((B, Lk, H, D), 62), _bf((B, Lk, H, D), 63)

@@ -247,6 +247,204 @@ struct TileLoader {
   }
 };
 
+// Per-wave state and tile arithmetic of the attention loop: the O^T accumulator,
+// the running reference max m_run (scale*log2(e) units) and this lane's partial row
+// sum l_run (its 32 keys of each tile), the Q fragments, and the lane-constant LDS
+// operand offsets.  Everything is force-inlined into the kernels that use it.
+struct TileCore {
+  f32x16 o[4];
+  float m_run;
+  float l_run;
+  float sl2;       // softmax scale * log2(e)
+  bf16x8 qf[8];    // B operand of S^T = K Q^T: query row lane % 32, channels 16 ks + 8 hh ..
+  int k_rd[8];
+  int v_rd[4];
+  int hh;
+
+  __device__ __forceinline__ void reset() {
+#pragma unroll
+    for (int md = 0; md < 4; ++md) o[md] = f32x16{};
+    m_run = -INFINITY;
+    l_run = 0.f;
+  }
+
+  __device__ __forceinline__ void set_offsets(int lane, float scale) {
+    const int n32 = lane & 31;
+    hh = lane >> 5;
+    sl2 = scale * kLog2e;
+    // rows n32 and 32 + n32 share the swizzle (row & 15): one offset per k-step
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) k_rd[ks] = n32 * D + (((2 * ks + hh) ^ k_swz(n32)) << 3);
+    const int tr_row = 4 * hh + ((lane & 15) >> 2);  // + 16*ksp + 8*r
+    const int tr_chunk = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);  // + 4*md
+    const int tr_sub = 4 * (lane & 1);
+    const int tr_x = v_swz(tr_row);  // (row & 3) is the same for every ksp, r
+#pragma unroll
+    for (int md = 0; md < 4; ++md) v_rd[md] = tr_row * D + (((4 * md + tr_chunk) ^ tr_x) << 3) + tr_sub;
+  }
+
+  // S^T of one 64-key tile: s0 holds keys 0..31, s1 keys 32..63 (accumulator row order)
+  __device__ __forceinline__ void qk(const bf16* Kt, f32x16& s0, f32x16& s1) const {
+    s0 = f32x16{};
+    s1 = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(Kt + k_rd[ks]);
+      const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(Kt + k_rd[ks] + 32 * D);
+      s0 = mfma32(a0, qf[ks], s0);
+      s1 = mfma32(a1, qf[ks], s1);
+    }
+  }
+
+  // P = exp2(S * scale*log2e - m_run) in bf16, and this lane's sum of P
+  // (of the bf16 values the PV MFMAs use; v_dot2 against (1, 1)).
+  // Used off the hot loop only (the last tile and the rescale path): each
+  // quarter of the tile is a scheduling region of its own, which bounds the
+  // exponentials in flight (and the register pressure) at eight.
+  __device__ __forceinline__ float exp_tile(const f32x16& s0, const f32x16& s1, bf16x8 pb[4]) const {
+    const bf16x2 one = {(bf16)1.0f, (bf16)1.0f};
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x16& sv = i < 2 ? s0 : s1;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pb[i][j] = (bf16)fast_exp2(fmaf(sv[8 * (i & 1) + j], sl2, -m_run));
+      acc[i] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pb[i], pb[i], 0, 1), one, acc[i], false);
+      acc[i] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pb[i], pb[i], 2, 3), one, acc[i], false);
+      acc[i] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pb[i], pb[i], 4, 5), one, acc[i], false);
+      acc[i] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pb[i], pb[i], 6, 7), one, acc[i], false);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    return (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  }
+
+  // Completes the softmax numerator of a tile whose P was computed against
+  // the current reference max with lane sum rs.  Only if some lane's sum
+  // exceeds kSumBound (or is inf / NaN: the first tile, where m_run is -inf)
+  // does the wave take the tile's exact row max, rescale O and l, and
+  // exponentiate again; afterwards every p <= 1.
+  __device__ __forceinline__ void finish(const f32x16& s0, const f32x16& s1, float rs, bf16x8 pb[4]) {
+    if (__builtin_amdgcn_ballot_w64(!(rs <= kSumBound)) != 0) {
+      float mx = fmaxf(s0[0], s0[1]);
+#pragma unroll
+      for (int r = 2; r < 16; ++r) mx = fmaxf(mx, s0[r]);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s1[r]);
+      const float m_new = fmaxf(m_run, pair_max(mx) * sl2);
+      const float alpha = fast_exp2(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int md = 0; md < 4; ++md) o[md] *= alpha;
+      rs = exp_tile(s0, s1, pb);
+    }
+    l_run += rs;
+  }
+
+  // Sets the scores of keys >= len to -inf (a partial last tile starting at key kt).
+  __device__ __forceinline__ void mask_tile(f32x16& s0, f32x16& s1, int kt, int len) const {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = kt + 8 * (r >> 2) + 4 * hh + (r & 3);
+      if (key >= len) s0[r] = -INFINITY;
+      if (key + 32 >= len) s1[r] = -INFINITY;
+    }
+  }
+
+  // The MFMAs of S(next) = K Q^T, interleaved in program order with the
+  // exponentials of the current tile's S (c0, c1): per k-step two MFMAs and
+  // elements 2ks, 2ks+1 of each half (4 fma + 4 exp2 + 2 cvt + 2 dot2).  K
+  // fragments are read one k-step ahead.  Returns this lane's sum of P.
+  __device__ __forceinline__ float qk_exp(const bf16* Kt, f32x16& n0, f32x16& n1, const f32x16& c0,
+                                          const f32x16& c1, bf16x8 pb[4]) const {
+    const bf16x2 one = {(bf16)1.0f, (bf16)1.0f};
+    float acc0 = 0.f, acc1 = 0.f;
+    bf16x8 a0 = *reinterpret_cast<const bf16x8*>(Kt + k_rd[0]);
+    bf16x8 a1 = *reinterpret_cast<const bf16x8*>(Kt + k_rd[0] + 32 * D);
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      bf16x8 b0, b1;
+      if (ks < 7) {
+        b0 = *reinterpret_cast<const bf16x8*>(Kt + k_rd[ks + 1]);
+        b1 = *reinterpret_cast<const bf16x8*>(Kt + k_rd[ks + 1] + 32 * D);
+      }
+      n0 = mfma32(a0, qf[ks], ks == 0 ? f32x16{} : n0);
+      n1 = mfma32(a1, qf[ks], ks == 0 ? f32x16{} : n1);
+      const int r = 2 * ks;
+      const bf16x2 u = {(bf16)fast_exp2(fmaf(c0[r], sl2, -m_run)),
+                        (bf16)fast_exp2(fmaf(c0[r + 1], sl2, -m_run))};
+      const bf16x2 w = {(bf16)fast_exp2(fmaf(c1[r], sl2, -m_run)),
+                        (bf16)fast_exp2(fmaf(c1[r + 1], sl2, -m_run))};
+      pb[ks >> 2][2 * (ks & 3)] = u[0];
+      pb[ks >> 2][2 * (ks & 3) + 1] = u[1];
+      pb[2 + (ks >> 2)][2 * (ks & 3)] = w[0];
+      pb[2 + (ks >> 2)][2 * (ks & 3) + 1] = w[1];
+      acc0 = __builtin_amdgcn_fdot2_f32_bf16(u, one, acc0, false);
+      acc1 = __builtin_amdgcn_fdot2_f32_bf16(w, one, acc1, false);
+      if (ks < 7) {
+        a0 = b0;
+        a1 = b1;
+      }
+    }
+    return acc0 + acc1;
+  }
+
+  // O^T += V^T P^T, V^T fragments read one MFMA ahead
+  __device__ __forceinline__ void pv(const bf16x8 pb[4], const bf16* Vt) {
+    auto vfrag = [&](int i) -> bf16x8 {
+      const bf16* vp = Vt + 16 * (i >> 2) * D + v_rd[i & 3];
+      const i16x4 lo = lds_read_tr(vp);
+      const i16x4 hi = lds_read_tr(vp + 8 * D);
+      return __builtin_bit_cast(bf16x8, (short __attribute__((ext_vector_type(8)))){
+                                            lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+    };
+    bf16x8 cur = vfrag(0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      bf16x8 nxt;
+      if (i < 15) nxt = vfrag(i + 1);
+      o[i & 3] = mfma32(cur, pb[i >> 2], o[i & 3]);
+      if (i < 15) cur = nxt;
+    }
+  }
+
+  // This wave's output tile (32 rows x 128 channels, divided by the row sum),
+  // staged through 4 KB of LDS at `stage` so that each store instruction writes
+  // whole 128-byte row segments (8 rows x 128 B) instead of 8-byte pieces of 32
+  // rows.  Two 64-channel halves; rows hold 8 chunks of 16 B, chunk c of row r at
+  // position c ^ (r & 7).  Non-temporal stores: the output is written once and not
+  // re-read here, so it should not displace K/V lines other workgroups still read.
+  __device__ __forceinline__ void store_out(bf16* stage, bf16* obase, int64_t o_st, int row0, int Lq,
+                                            int lane) const {
+    const int n32 = lane & 31, half_lane = lane >> 5;   // (set_offsets may not have run)
+    const float l_tot = pair_sum(l_run);
+    const float inv_l = l_tot > 0.f ? 1.f / l_tot : 0.f;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+#pragma unroll
+      for (int mm = 0; mm < 2; ++mm) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          bf16x4 w;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[e] = (bf16)(o[2 * half + mm][4 * g + e] * inv_l);
+          const int c = 4 * mm + g;  // lane holds channels 8c + 4hh .. +3 of row n32
+          *reinterpret_cast<bf16x4*>(stage + n32 * 64 + ((c ^ (n32 & 7)) << 3) + 4 * half_lane) = w;
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = 8 * j + (lane >> 3), c = lane & 7;
+        const bf16x8 v = *reinterpret_cast<const bf16x8*>(stage + r * 64 + ((c ^ (r & 7)) << 3));
+        if (row0 + r < Lq)
+          __builtin_nontemporal_store(v, reinterpret_cast<bf16x8*>(obase + (int64_t)(row0 + r) * o_st + 64 * half + 8 * c));
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+  }
+};
+
 template <int NW, int QP>
 __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a) {
   constexpr int BM = NW * 32;
@@ -291,11 +489,8 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
   const int ntiles = (len + BN - 1) / BN;
 
   const int qrow = mblk * BM + wave * 32 + n32;
-  f32x16 o[4];
-#pragma unroll
-  for (int md = 0; md < 4; ++md) o[md] = f32x16{};
-  float m_run = -INFINITY;  // running reference max, in scale*log2(e) units
-  float l_run = 0.f;        // this lane's partial row sum (its 32 keys of each tile)
+  TileCore c;
+  c.reset();
 
   if (ntiles > 0) {
     TileLoader<NW> kl, vl;
@@ -305,7 +500,6 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
     // back per lane.  With the ring of four they use buffers 1-3 and the extra
     // 32 KB while K0 and V0 are already being copied; with two buffers they use
     // all of them and the tiles follow.
-    bf16x8 qf[8];
     if constexpr (QP == kQNormRope) {
       const int row0w = mblk * BM + wave * 32;
       bf16 *cos_st, *sin_st;
@@ -320,7 +514,7 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
       }
       stage_rows32(reinterpret_cast<const char*>(a.cos), kRopePairs * 4, row0w, a.Lq - 1, cos_st, lane);
       stage_rows32(reinterpret_cast<const char*>(a.sin), kRopePairs * 4, row0w, a.Lq - 1, sin_st, lane);
-      load_q_fragment<QP>(a, b, h, qrow, hh, qf, reinterpret_cast<const char*>(cos_st),
+      load_q_fragment<QP>(a, b, h, qrow, hh, c.qf, reinterpret_cast<const char*>(cos_st),
                           reinterpret_cast<const char*>(sin_st), n32);
       // every wave's staging copies have landed (also those of a wave whose rows
       // are all past Lq) and every wave is done reading them before tiles are
@@ -347,7 +541,7 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
       bf16* q_st = &v_lds[0][0] + wave * 4096;
       stage_rows32(reinterpret_cast<const char*>(a.q.ptr + b * a.q.sb + h * a.q.sh), a.q.st * 2, row0w,
                    a.Lq - 1, q_st, lane);
-      load_q_fragment<QP>(a, b, h, qrow, hh, qf, nullptr, nullptr, n32, reinterpret_cast<const char*>(q_st));
+      load_q_fragment<QP>(a, b, h, qrow, hh, c.qf, nullptr, nullptr, n32, reinterpret_cast<const char*>(q_st));
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();  // every wave is done with its staged rows before V0 lands there
       vl.issue(0, len, v_lds[0], wave, lane);
@@ -358,147 +552,10 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
       if (ntiles > 1) kl.issue(1, len, k_lds[1], wave, lane);
       if (ntiles > 1) vl.issue(1, len, v_lds[1], wave, lane);
       if (ntiles > 2) kl.issue(2, len, k_lds[2], wave, lane);
-      load_q_fragment<QP>(a, b, h, qrow, hh, qf, nullptr, nullptr, n32);
+      load_q_fragment<QP>(a, b, h, qrow, hh, c.qf, nullptr, nullptr, n32);
     }
 
-    const float sl2 = a.scale * kLog2e;
-
-    // lane-constant LDS operand offsets (elements)
-    // rows n32 and 32 + n32 share the swizzle (row & 15): one offset per k-step
-    int k_rd[8];
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) k_rd[ks] = n32 * D + (((2 * ks + hh) ^ k_swz(n32)) << 3);
-    const int tr_row = 4 * hh + ((lane & 15) >> 2);  // + 16*ksp + 8*r
-    const int tr_chunk = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);  // + 4*md
-    const int tr_sub = 4 * (lane & 1);
-    const int tr_x = v_swz(tr_row);  // (row & 3) is the same for every ksp, r
-    int v_rd[4];
-#pragma unroll
-    for (int md = 0; md < 4; ++md) v_rd[md] = tr_row * D + (((4 * md + tr_chunk) ^ tr_x) << 3) + tr_sub;
-
-    auto qk = [&](const bf16* Kt, f32x16& s0, f32x16& s1) {
-      s0 = f32x16{};
-      s1 = f32x16{};
-#pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
-        const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(Kt + k_rd[ks]);
-        const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(Kt + k_rd[ks] + 32 * D);
-        s0 = mfma32(a0, qf[ks], s0);
-        s1 = mfma32(a1, qf[ks], s1);
-      }
-    };
-
-    // P = exp2(S * scale*log2e - m_run) in bf16, and this lane's sum of P
-    // (of the bf16 values the PV MFMAs use; v_dot2 against (1, 1)).
-    // Used off the hot loop only (the last tile and the rescale path): each
-    // quarter of the tile is a scheduling region of its own, which bounds the
-    // exponentials in flight (and the register pressure) at eight.
-    auto exp_tile = [&](const f32x16& s0, const f32x16& s1, bf16x8 pb[4]) -> float {
-      const bf16x2 one = {(bf16)1.0f, (bf16)1.0f};
-      float acc[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const f32x16& sv = i < 2 ? s0 : s1;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) pb[i][j] = (bf16)fast_exp2(fmaf(sv[8 * (i & 1) + j], sl2, -m_run));
-        acc[i] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pb[i], pb[i], 0, 1), one, acc[i], false);
-        acc[i] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pb[i], pb[i], 2, 3), one, acc[i], false);
-        acc[i] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pb[i], pb[i], 4, 5), one, acc[i], false);
-        acc[i] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pb[i], pb[i], 6, 7), one, acc[i], false);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      return (acc[0] + acc[1]) + (acc[2] + acc[3]);
-    };
-
-    // Completes the softmax numerator of a tile whose P was computed against
-    // the current reference max with lane sum rs.  Only if some lane's sum
-    // exceeds kSumBound (or is inf / NaN: the first tile, where m_run is -inf)
-    // does the wave take the tile's exact row max, rescale O and l, and
-    // exponentiate again; afterwards every p <= 1.
-    auto finish = [&](const f32x16& s0, const f32x16& s1, float rs, bf16x8 pb[4]) {
-      if (__builtin_amdgcn_ballot_w64(!(rs <= kSumBound)) != 0) {
-        float mx = fmaxf(s0[0], s0[1]);
-#pragma unroll
-        for (int r = 2; r < 16; ++r) mx = fmaxf(mx, s0[r]);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s1[r]);
-        const float m_new = fmaxf(m_run, pair_max(mx) * sl2);
-        const float alpha = fast_exp2(m_run - m_new);
-        m_run = m_new;
-        l_run *= alpha;
-#pragma unroll
-        for (int md = 0; md < 4; ++md) o[md] *= alpha;
-        rs = exp_tile(s0, s1, pb);
-      }
-      l_run += rs;
-    };
-
-    // Sets the scores of keys >= len to -inf (a partial last tile starting at key kt).
-    auto mask_tile = [&](f32x16& s0, f32x16& s1, int kt) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kt + 8 * (r >> 2) + 4 * hh + (r & 3);
-        if (key >= len) s0[r] = -INFINITY;
-        if (key + 32 >= len) s1[r] = -INFINITY;
-      }
-    };
-
-    // The MFMAs of S(next) = K Q^T, interleaved in program order with the
-    // exponentials of the current tile's S (c0, c1): per k-step two MFMAs and
-    // elements 2ks, 2ks+1 of each half (4 fma + 4 exp2 + 2 cvt + 2 dot2).  K
-    // fragments are read one k-step ahead.  Returns this lane's sum of P.
-    auto qk_exp = [&](const bf16* Kt, f32x16& n0, f32x16& n1, const f32x16& c0, const f32x16& c1,
-                      bf16x8 pb[4]) -> float {
-      const bf16x2 one = {(bf16)1.0f, (bf16)1.0f};
-      float acc0 = 0.f, acc1 = 0.f;
-      bf16x8 a0 = *reinterpret_cast<const bf16x8*>(Kt + k_rd[0]);
-      bf16x8 a1 = *reinterpret_cast<const bf16x8*>(Kt + k_rd[0] + 32 * D);
-#pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
-        bf16x8 b0, b1;
-        if (ks < 7) {
-          b0 = *reinterpret_cast<const bf16x8*>(Kt + k_rd[ks + 1]);
-          b1 = *reinterpret_cast<const bf16x8*>(Kt + k_rd[ks + 1] + 32 * D);
-        }
-        n0 = mfma32(a0, qf[ks], ks == 0 ? f32x16{} : n0);
-        n1 = mfma32(a1, qf[ks], ks == 0 ? f32x16{} : n1);
-        const int r = 2 * ks;
-        const bf16x2 u = {(bf16)fast_exp2(fmaf(c0[r], sl2, -m_run)),
-                          (bf16)fast_exp2(fmaf(c0[r + 1], sl2, -m_run))};
-        const bf16x2 w = {(bf16)fast_exp2(fmaf(c1[r], sl2, -m_run)),
-                          (bf16)fast_exp2(fmaf(c1[r + 1], sl2, -m_run))};
-        pb[ks >> 2][2 * (ks & 3)] = u[0];
-        pb[ks >> 2][2 * (ks & 3) + 1] = u[1];
-        pb[2 + (ks >> 2)][2 * (ks & 3)] = w[0];
-        pb[2 + (ks >> 2)][2 * (ks & 3) + 1] = w[1];
-        acc0 = __builtin_amdgcn_fdot2_f32_bf16(u, one, acc0, false);
-        acc1 = __builtin_amdgcn_fdot2_f32_bf16(w, one, acc1, false);
-        if (ks < 7) {
-          a0 = b0;
-          a1 = b1;
-        }
-      }
-      return acc0 + acc1;
-    };
-
-    // O^T += V^T P^T, V^T fragments read one MFMA ahead
-    auto pv = [&](const bf16x8 pb[4], const bf16* Vt) {
-      auto vfrag = [&](int i) -> bf16x8 {
-        const bf16* vp = Vt + 16 * (i >> 2) * D + v_rd[i & 3];
-        const i16x4 lo = lds_read_tr(vp);
-        const i16x4 hi = lds_read_tr(vp + 8 * D);
-        return __builtin_bit_cast(bf16x8, (short __attribute__((ext_vector_type(8)))){
-                                              lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
-      };
-      bf16x8 cur = vfrag(0);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        bf16x8 nxt;
-        if (i < 15) nxt = vfrag(i + 1);
-        o[i & 3] = mfma32(cur, pb[i >> 2], o[i & 3]);
-        if (i < 15) cur = nxt;
-      }
-    };
+    c.set_offsets(lane, a.scale);
 
     // One pipelined step on tile t (not the last tile): the loads of K(t+2)
     // and V(t+1); the MFMAs of S(t+1) = K(t+1) Q^T, the softmax of S(t) and
@@ -509,8 +566,8 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
       if (t + 2 < ntiles) kl.issue(t + 2, len, k_fill, wave, lane);
       vl.issue(t + 1, len, v_fill, wave, lane);
       bf16x8 pb[4];
-      finish(c0, c1, qk_exp(k_next, n0, n1, c0, c1, pb), pb);
-      pv(pb, v_cur);
+      c.finish(c0, c1, c.qk_exp(k_next, n0, n1, c0, c1, pb), pb);
+      c.pv(pb, v_cur);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
     };
@@ -520,14 +577,14 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
       // the staging barrier published the first K tile(s) (and V0 with the
       // ring of four); the tiles issued after it land while S(0) is computed,
       // and this barrier publishes them and frees K0
-      qk(k_lds[0], sa0, sa1);
+      c.qk(k_lds[0], sa0, sa1);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
     } else {
       // prologue: S(0) once the first tiles have landed
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
-      qk(k_lds[0], sa0, sa1);
+      c.qk(k_lds[0], sa0, sa1);
       __syncthreads();  // every wave is done with K0 before it is overwritten
     }
 
@@ -562,8 +619,8 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
           if (t + 3 < ntiles) vl.issue(t + 3, len, vf3, wave, lane);
         }
         bf16x8 pb[4];
-        finish(c0, c1, qk_exp(k_next, n0, n1, c0, c1, pb), pb);
-        pv(pb, v_cur);
+        c.finish(c0, c1, c.qk_exp(k_next, n0, n1, c0, c1, pb), pb);
+        c.pv(pb, v_cur);
         if (odd) {
           asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
           __syncthreads();
@@ -586,52 +643,19 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
       v_last = v_lds[t & 3];
     }
     // the last tile, its keys >= len masked when it is partial
-    if (ntiles * BN > len) mask_tile(sa0, sa1, t * BN);
+    if (ntiles * BN > len) c.mask_tile(sa0, sa1, t * BN, len);
     bf16x8 pb[4];
-    finish(sa0, sa1, exp_tile(sa0, sa1, pb), pb);
-    pv(pb, v_last);
+    c.finish(sa0, sa1, c.exp_tile(sa0, sa1, pb), pb);
+    c.pv(pb, v_last);
     // the output staging below overwrites K buffers that a slower wave may
     // still read in its last step when that step ended without a barrier
     if constexpr (RING == 4) __syncthreads();
   }
 
-  const float l_tot = pair_sum(l_run);
-  const float inv_l = l_tot > 0.f ? 1.f / l_tot : 0.f;
-
-  // Output store, staged through LDS so that each store instruction writes
-  // whole 128-byte row segments (8 rows x 128 B) instead of 8-byte pieces of
-  // 32 rows.  The K buffers are free here: their last reads came before the
-  // last barrier, and no load into them is in flight.  Each wave owns 4 KB
-  // (32 rows x 64 channels) and writes its 128 channels in two halves; rows
-  // hold 8 chunks of 16 B, chunk c of row r at position c ^ (r & 7).  The
-  // stores are non-temporal: the output is written once and not re-read here,
-  // so it should not displace the K/V lines that other workgroups still read.
+  // Output store, staged through the K buffers: they are free here (their last
+  // reads came before the last barrier, and no load into them is in flight).
   bf16* stage = (wave < 4 ? k_lds[0] : k_lds[1]) + (wave & 3) * 2048;
-  const int row0 = mblk * BM + wave * 32;
-  bf16* obase = a.o + b * a.o_sb + h * a.o_sh;
-#pragma unroll
-  for (int half = 0; half < 2; ++half) {
-#pragma unroll
-    for (int mm = 0; mm < 2; ++mm) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        bf16x4 w;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) w[e] = (bf16)(o[2 * half + mm][4 * g + e] * inv_l);
-        const int c = 4 * mm + g;  // lane holds channels 8c + 4hh .. +3 of row n32
-        *reinterpret_cast<bf16x4*>(stage + n32 * 64 + ((c ^ (n32 & 7)) << 3) + 4 * hh) = w;
-      }
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int r = 8 * j + (lane >> 3), c = lane & 7;
-      const bf16x8 v = *reinterpret_cast<const bf16x8*>(stage + r * 64 + ((c ^ (r & 7)) << 3));
-      if (row0 + r < a.Lq)
-        __builtin_nontemporal_store(v, reinterpret_cast<bf16x8*>(obase + (int64_t)(row0 + r) * a.o_st + 64 * half + 8 * c));
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  }
+  c.store_out(stage, a.o + b * a.o_sb + h * a.o_sh, a.o_st, mblk * BM + wave * 32, a.Lq, lane);
 }
 
 // Explicit instantiations: without them clang emits the host launch stubs of
@@ -642,6 +666,223 @@ template __global__ void flash_fwd_kernel<kWaves, kQNormRope>(const FlashArgs);
 template __global__ void flash_fwd_kernel<4, kQPlain>(const FlashArgs);
 template __global__ void flash_fwd_kernel<4, kQNorm>(const FlashArgs);
 template __global__ void flash_fwd_kernel<4, kQNormRope>(const FlashArgs);
+
+// ---------------------------------------------------------------------------
+// Short keys (<= kShortKeys, the cross-attention's text keys) with per-sample key
+// lengths and no RoPE on the query: a persistent kernel.  A workgroup has 4 waves
+// (128 query rows of one (batch, head) per item) and two run per CU.  Items of a
+// short sample are mostly start-up (query rows, first K/V tiles) and output store;
+// here, once an item's last S MFMAs are done, the next item's first two K tiles are
+// copied into the (then free) K buffers and its query rows loaded into the (then
+// free) Q registers, so that start-up overlaps the item's last tile and output store.
+// The output goes through LDS of its own (16 KB), so the K buffers can take the next
+// item's tiles meanwhile.  Each XCD owns a contiguous chunk of the items (a (batch,
+// head)'s K/V stay in one L2), its W workgroups striding through the chunk; the
+// batch index varies fastest over the items and W is odd, so consecutive items of a
+// workgroup alternate between the samples and long and short ones spread evenly.
+// ---------------------------------------------------------------------------
+
+struct ShortItem {
+  int b, h, mblk, len, ntiles;
+};
+
+__device__ __forceinline__ ShortItem short_item(const FlashArgs& a, int it, int num_m) {
+  ShortItem r;
+  r.b = it % a.B;
+  const int rest = it / a.B;
+  r.mblk = rest % num_m;
+  r.h = rest / num_m;
+  r.len = a.seqlen_k != nullptr ? min(max(a.seqlen_k[r.b], 0), a.Lk) : a.seqlen_all;
+  r.ntiles = (r.len + BN - 1) / BN;
+  return r;
+}
+
+// Raw query fragment of `row` (zeros past Lq) and, with the Q norm, its inverse RMS.
+template <int QP>
+__device__ __forceinline__ void load_q_raw(const FlashArgs& a, int b, int h, int row, int hh,
+                                           bf16x8 qf[8], float& inv) {
+  if (row >= a.Lq) {
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) qf[ks] = bf16x8{};
+    inv = 0.f;
+    return;
+  }
+  const bf16* qp = a.q.ptr + b * a.q.sb + (int64_t)row * a.q.st + h * a.q.sh;
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(qp + 16 * ks + 8 * hh);
+  inv = QP != kQPlain ? a.inv_rms_q[(int64_t)b * a.Lq + row] : 1.f;
+}
+
+// q' = bf16(bf16(q * inv_rms) * gamma), the reference's rounding points
+// (models/fast_dit.py:145-146, 156-160).
+__device__ __forceinline__ void norm_q(const FlashArgs& a, int h, int hh, float inv, bf16x8 qf[8]) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) {
+    const bf16x8 g = *reinterpret_cast<const bf16x8*>(a.gamma_q + h * D + 16 * ks + 8 * hh);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const bf16 t = (bf16)((float)qf[ks][j] * inv);
+      qf[ks][j] = (bf16)((float)t * (float)g[j]);
+    }
+  }
+}
+
+// The kernel's own argument block, re-read from the kernarg segment (scalar loads,
+// scalar-cache hits).  The empty asm hides the pointer's value from the compiler, so
+// the fields are loaded where they are used instead of being held in SGPRs across
+// the whole persistent loop (where they did not fit and were spilled).
+__device__ __forceinline__ const FlashArgs& kernel_args() {
+  const __attribute__((address_space(4))) char* p =
+      (const __attribute__((address_space(4))) char*)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(p));
+  return *reinterpret_cast<const FlashArgs*>((const char*)p);
+}
+
+template <int QP>
+__global__ __launch_bounds__(256, 2) void flash_short_kernel(const FlashArgs a0, int num_items) {
+  constexpr int NW = 4, BM = NW * 32;
+  __shared__ __attribute__((aligned(1024))) bf16 k_lds[2][kTileElems];
+  __shared__ __attribute__((aligned(1024))) bf16 v_lds[2][kTileElems];
+  __shared__ __attribute__((aligned(1024))) bf16 o_lds[NW * 2048];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n32 = lane & 31, hh = lane >> 5;
+  const int num_m = (a0.Lq + BM - 1) / BM;
+
+  TileCore c;
+  c.set_offsets(lane, a0.scale);
+  TileLoader<NW> kl, vl;
+  kl.init(a0.k.ptr, a0.k.st, wave, lane, true);
+  vl.init(a0.v.ptr, a0.v.st, wave, lane, false);
+
+  // An item's first two K tiles (global -> LDS copies into the free K buffers).
+  auto prefetch_k = [&](const FlashArgs& a, const ShortItem& it) {
+    if (it.ntiles > 0) {
+      kl.base = reinterpret_cast<const char*>(a.k.ptr + it.b * a.k.sb + it.h * a.k.sh);
+      kl.issue(0, it.len, k_lds[0], wave, lane);
+      if (it.ntiles > 1) kl.issue(1, it.len, k_lds[1], wave, lane);
+    }
+  };
+
+  // Each XCD (workgroup id % 8) owns one contiguous chunk of the items, so the
+  // K/V of a (batch, head) are fetched into one XCD's L2; the W workgroups of an
+  // XCD stride through its chunk.
+  const int xcd = blockIdx.x % kNumXcd, per = gridDim.x / kNumXcd;
+  const int base_n = num_items / kNumXcd, extra = num_items % kNumXcd;
+  const int chunk_end = (xcd + 1) * base_n + min(xcd + 1, extra);
+  int it = xcd * base_n + min(xcd, extra) + (int)(blockIdx.x / kNumXcd);
+  if (it >= chunk_end) return;
+  ShortItem cur = short_item(a0, it, num_m);
+  float inv = 1.f;
+  prefetch_k(a0, cur);
+  load_q_raw<QP>(a0, cur.b, cur.h, cur.mblk * BM + wave * 32 + n32, hh, c.qf, inv);
+  for (;;) {
+    c.reset();
+    if constexpr (QP != kQPlain) norm_q(kernel_args(), cur.h, hh, inv, c.qf);
+    const int nit = it + per;
+    if (cur.ntiles > 0) {
+      {
+        const FlashArgs& a = kernel_args();
+        vl.base = reinterpret_cast<const char*>(a.v.ptr + cur.b * a.v.sb + cur.h * a.v.sh);
+      }
+      // this item's K0 / K1 (and query rows) have landed, for every wave; every
+      // wave is done with the previous item's V tiles
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      vl.issue(0, cur.len, v_lds[0], wave, lane);
+      f32x16 sa0, sa1, sb0, sb1;
+      // V0 lands while S(0) is computed; the barrier publishes it and frees K0
+      c.qk(k_lds[0], sa0, sa1);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+
+      auto step = [&](int t, bf16* k_fill, bf16* v_fill, const bf16* k_next, const bf16* v_cur,
+                      f32x16& c0, f32x16& c1, f32x16& n0, f32x16& n1) {
+        if (t + 2 < cur.ntiles) kl.issue(t + 2, cur.len, k_fill, wave, lane);
+        vl.issue(t + 1, cur.len, v_fill, wave, lane);
+        bf16x8 pb[4];
+        c.finish(c0, c1, c.qk_exp(k_next, n0, n1, c0, c1, pb), pb);
+        c.pv(pb, v_cur);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+      };
+      int t = 0;
+      const bf16* v_last = v_lds[0];
+      for (; t + 2 < cur.ntiles; t += 2) {
+        step(t, k_lds[0], v_lds[1], k_lds[1], v_lds[0], sa0, sa1, sb0, sb1);
+        step(t + 1, k_lds[1], v_lds[0], k_lds[0], v_lds[1], sb0, sb1, sa0, sa1);
+      }
+      if (t + 1 < cur.ntiles) {
+        step(t, k_lds[0], v_lds[1], k_lds[1], v_lds[0], sa0, sa1, sb0, sb1);
+        sa0 = sb0;
+        sa1 = sb1;
+        v_last = v_lds[1];
+        ++t;
+      }
+      // Every wave has passed the barrier after the last S MFMAs: the K buffers
+      // are free for the next item's first tiles.
+      if (nit < chunk_end) {
+        const FlashArgs& a = kernel_args();
+        const ShortItem ni = short_item(a, nit, num_m);
+        prefetch_k(a, ni);
+        load_q_raw<QP>(a, ni.b, ni.h, ni.mblk * BM + wave * 32 + n32, hh, c.qf, inv);
+      }
+      if (cur.ntiles * BN > cur.len) c.mask_tile(sa0, sa1, t * BN, cur.len);
+      bf16x8 pb[4];
+      c.finish(sa0, sa1, c.exp_tile(sa0, sa1, pb), pb);
+      c.pv(pb, v_last);
+    } else if (nit < chunk_end) {
+      const FlashArgs& a = kernel_args();
+      prefetch_k(a, short_item(a, nit, num_m));
+    }
+    // The next item's query rows go into the Q registers (free now) before this
+    // item's output is normalised and stored, so their loads overlap the store.
+    const FlashArgs& a = kernel_args();
+    ShortItem nxt{};
+    if (nit < chunk_end) {
+      nxt = short_item(a, nit, num_m);
+      if (cur.ntiles == 0) load_q_raw<QP>(a, nxt.b, nxt.h, nxt.mblk * BM + wave * 32 + n32, hh, c.qf, inv);
+    }
+    c.store_out(o_lds + wave * 2048, a.o + cur.b * a.o_sb + cur.h * a.o_sh, a.o_st,
+                cur.mblk * BM + wave * 32, a.Lq, lane);
+    if (nit >= chunk_end) break;
+    it = nit;
+    cur = nxt;
+  }
+}
+
+template __global__ void flash_short_kernel<kQPlain>(const FlashArgs, int);
+template __global__ void flash_short_kernel<kQNorm>(const FlashArgs, int);
+
+// Workgroups of the persistent kernel: kNumXcd x W, W per XCD, at most two per CU
+// and odd (so that one workgroup's consecutive items alternate between the samples
+// of a batch of 2).
+int short_grid(int items) {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  int w = 2 * (cus[dev] / kNumXcd);
+  w = w > 1 ? w - 1 : 1;
+  const int need = (items + kNumXcd - 1) / kNumXcd;
+  return kNumXcd * (need < w ? need : w);
+}
+
+template <int QP>
+int launch_short(const FlashArgs& a, hipStream_t s) {
+  const int64_t items = (int64_t)((a.Lq + 127) / 128) * a.B * a.H;
+  if (items > 0x7fffffff) return set_error(2, "flash_fwd: %lld items too many", (long long)items);
+  hipLaunchKernelGGL((flash_short_kernel<QP>), dim3(short_grid((int)items)), dim3(256), 0, s, a, (int)items);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : set_error(4, "flash_fwd launch: %s", hipGetErrorString(e));
+}
 
 template <int NW, int QP>
 int launch_nw(const FlashArgs& a, hipStream_t s) {
@@ -660,9 +901,21 @@ int launch_nw(const FlashArgs& a, hipStream_t s) {
 // tiles (measured 5% faster at 512 keys; equal or slower from 1080 keys on).
 constexpr int kShortKeys = 1024;
 
+// With per-sample key lengths the items of a short-key call differ in cost, and
+// those of the short samples are mostly start-up: there the persistent kernel,
+// which hides each item's start-up behind the previous item, is measured 13%
+// faster (lengths 470 / 123 at Lq 7854: 87 vs 100 us).  With one key length for
+// all (every item the same few tiles) the hardware's own dispatch overlaps one
+// workgroup's start-up with the other's tiles as well, and the plain kernel is
+// 5% faster (512 keys: 109 vs 115 us).
 template <int QP>
 int launch_qp(const FlashArgs& a, hipStream_t s) {
-  if (a.Lk <= kShortKeys) return launch_nw<4, QP>(a, s);
+  if (a.Lk <= kShortKeys) {
+    if constexpr (QP != kQNormRope) {
+      if (a.seqlen_k != nullptr) return launch_short<QP>(a, s);
+    }
+    return launch_nw<4, QP>(a, s);
+  }
   return launch_nw<kWaves, QP>(a, s);
 }
 
