@@ -11,8 +11,9 @@ attention, on seeded N(0,1) projections already resident in HBM.
   roofline    the attention kernel alone: algorithmic FLOPs / its average launch
               time (HIP events around its launch on the stream it runs on), against
               MI355X dense bf16 MFMA peak (2.5 PFLOP/s)
-  cpu_baseline  the oracle's torch SDPA (fp32) on the host cores, on a bounded sample
-              of (batch, head) pairs of the same workload
+  cpu_baseline  the reference's SDPA path (restated by the oracle: QK-RMSNorm + RoPE +
+              torch SDPA) on the host cores over the whole config C workload in fp32,
+              median of up to 3 runs; configs A and B and bf16 under "table"
   extra       the same path at L=1080 and the masked cross-attention (Lq=7854,
               512 text keys, per-sample lengths U[16, 512]), with HBM GB/s; torch's
               own flash SDPA on the config C shapes, for comparison; one
@@ -21,6 +22,7 @@ attention, on seeded N(0,1) projections already resident in HBM.
 
 Prints one JSON line on stdout.  Usage:
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--cpu-seconds S] [--no-cpu-baseline]
+  python bench.py --profile-config {A,B,C} [--steps K]   (one config's steps only, for rocprofv3)
 """
 import argparse
 import json
@@ -44,18 +46,37 @@ def log(*a):
 
 
 TRAFFIC_PROFILE = os.path.join("profiles", "flash_fwd_selfattn_L7854.md")
+KERNEL_SOURCES = [os.path.join("wan2-ti2v-5b_amd", "csrc", f) for f in ("common.h", "flash_fwd.hip")]
+
+
+def kernel_source_hash():
+    """sha256 over the attention kernel's sources (common.h, flash_fwd.hip)."""
+    import hashlib
+    h = hashlib.sha256()
+    for f in KERNEL_SOURCES:
+        with open(os.path.join(ROOT, f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()
 
 
 def profiled_traffic():
     """HBM bytes per launch of the config C attention kernel, from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE summary (calibrated against a plain copy), or None."""
+    FETCH_SIZE / WRITE_SIZE summary (calibrated against a plain copy), and a note.  The
+    summary records the hash of the kernel sources it measured; when the sources differ
+    the figure is stale and None is returned."""
     import re
     try:
         text = open(os.path.join(ROOT, TRAFFIC_PROFILE)).read()
     except OSError:
-        return None
+        return None, "no traffic profile"
     m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", text, re.M)
-    return int(m.group(1)) if m else None
+    hm = re.search(r"^kernel_source_sha256:\s*([0-9a-f]{64})", text, re.M)
+    if not m:
+        return None, "no traffic figure in " + TRAFFIC_PROFILE
+    if not hm or hm.group(1) != kernel_source_hash():
+        return None, ("stale: " + TRAFFIC_PROFILE + " measured other kernel sources "
+                      "(kernel_source_sha256 differs)")
+    return int(m.group(1)), TRAFFIC_PROFILE + " (FETCH_SIZE x2.0 + WRITE_SIZE x1.0, per launch)"
 
 
 def attn_flops(b, h, lq, lk):
@@ -152,6 +173,9 @@ def bench_cross(torch, W, dev, steps, warmup):
                                                   None, None, D ** -0.5, lens_d.data_ptr(), s))
     total, (t_prep, t_attn) = time_steps(torch, [prep, attn], steps, warmup)
     ssum = int(lens.sum())
+    host = dict(q=q.cpu(), ck=ck.cpu(), cv=cv.cpu(), gq=gq.cpu(), lens=lens.tolist(),
+                flops=4.0 * H * Lq * D * ssum,
+                workload=f"cross-attn B=2 Lq={Lq} Lkv={L_TEXT} seqlen_k={lens.tolist()}")
     flops = 4.0 * H * Lq * D * ssum
     byts = 2 * (B * Lq * H * D * 2) + 2 * ssum * H * D * 2   # q read, o write, k+v rows read
     return {
@@ -160,7 +184,7 @@ def bench_cross(torch, W, dev, steps, warmup):
         "tflops_kernel": flops / (t_attn * 1e-3) / 1e12,
         "hbm_gbs_kernel": byts / (t_attn * 1e-3) / 1e9,
         "frac_hbm_peak": byts / (t_attn * 1e-3) / 1e9 / PEAK_HBM_GBS,
-    }
+    }, host
 
 
 def bench_torch_sdpa(torch, t, steps, warmup):
@@ -238,34 +262,63 @@ def bench_dit(torch, W, dev, steps, layers):
     }
 
 
-def cpu_baseline(torch, host, seconds):
-    """fp32 torch SDPA (the oracle) on the host cores: QK-RMSNorm + RoPE over all tokens,
-    then SDPA on (batch, head) pairs until `seconds` of CPU work are done."""
+def cpu_baseline(torch, hosts, seconds):
+    """The reference's SDPA path (models/fast_dit.py:186-189, restated by the oracle) on the
+    host cores, in fp32 and in bf16, for configs C, A and B on the GPU run's own inputs:
+    QK-RMSNorm + RoPE + SDPA over every (batch, head) for the self-attention, Q-RMSNorm +
+    masked SDPA for the cross-attention.  Each is the median of up to 3 repetitions (after
+    one warm-up for A and B), within about `seconds` of CPU work in all; config C in fp32,
+    the headline workload, always gets at least one.  Returns the headline object (config C,
+    fp32) with the whole table under "table"."""
     sys.path.insert(0, ROOT)
     from oracle import ref
-    threads = os.cpu_count() or 1
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
     torch.set_num_threads(threads)
-    q, k, v = (host[n].float() for n in "qkv")
-    L = q.shape[1]
-    t0 = time.perf_counter()
-    qn, kn = ref.rms_qk(q.reshape(B, L, H * D), k.reshape(B, L, H * D), host["gq"].float(), host["gk"].float())
-    qr = ref.rope(qn.view(B, L, H, D), host["cos"], host["sin"])
-    kr = ref.rope(kn.view(B, L, H, D), host["cos"], host["sin"])
-    t_prep = time.perf_counter() - t0
-    pairs, t_attn = 0, 0.0
-    while t_attn < seconds:
-        b, h = divmod(pairs % (B * H), H)
-        t1 = time.perf_counter()
-        ref.sdpa(qr[b:b + 1, :, h:h + 1], kr[b:b + 1, :, h:h + 1], v[b:b + 1, :, h:h + 1])
-        t_attn += time.perf_counter() - t1
-        pairs += 1
-    flops = pairs * 4.0 * L * L * D
-    t = t_attn + t_prep * pairs / (B * H)
+
+    def self_path(h, dt):
+        q, k, v = (h[n].to(dt) for n in "qkv")
+        Bn, L, Hn, Dd = q.shape
+        qn, kn = ref.rms_qk(q.reshape(Bn, L, Hn * Dd), k.reshape(Bn, L, Hn * Dd), h["gq"].to(dt), h["gk"].to(dt))
+        return ref.sdpa(ref.rope(qn.view(Bn, L, Hn, Dd), h["cos"], h["sin"]),
+                        ref.rope(kn.view(Bn, L, Hn, Dd), h["cos"], h["sin"]), v)
+
+    def cross_path(h, dt):
+        q, ck, cv = (h[n].to(dt) for n in ("q", "ck", "cv"))
+        Bn, L, Hn, Dd = q.shape
+        qn = ref.rms(q.reshape(Bn, L, Hn * Dd), h["gq"].to(dt)).view(Bn, L, Hn, Dd)
+        return ref.sdpa(qn, ck, cv, seqlen_k=h["lens"])
+
+    plan = [("C", torch.float32, 3), ("A", torch.float32, 3), ("B", torch.float32, 3),
+            ("A", torch.bfloat16, 3), ("B", torch.bfloat16, 3), ("C", torch.bfloat16, 3)]
+    table, spent = {}, 0.0
+    for cfg, dt, reps in plan:
+        h = hosts.get(cfg)
+        if h is None:
+            continue
+        fn = cross_path if cfg == "B" else self_path
+        if cfg != "C":
+            fn(h, dt)
+        times = []
+        for r in range(reps):
+            if spent >= seconds and not (cfg == "C" and dt == torch.float32 and r == 0):
+                break
+            t0 = time.perf_counter()
+            fn(h, dt)
+            times.append(time.perf_counter() - t0)
+            spent += times[-1]
+        if not times:
+            continue
+        med = sorted(times)[len(times) // 2]
+        key = f"{cfg}_{'fp32' if dt == torch.float32 else 'bf16'}"
+        table[key] = {"ms": med * 1e3, "tflops": h["flops"] / med / 1e12, "reps": len(times),
+                      "workload": h["workload"]}
+    c = table["C_fp32"]
     return {
-        "value": flops / t / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-        "sample": f"fp32 torch SDPA (oracle/ref.py) over {pairs} (batch, head) pairs, cycling "
-                  f"through the {B * H} of the L={L} workload, all queries x all keys, plus "
-                  f"QK-RMSNorm/RoPE over all tokens pro rata; {t:.1f} s of CPU work",
+        "value": c["tflops"], "unit": "TFLOP/s", "cores": threads, "kind": "port",
+        "sample": f"the whole config C workload (B=2, L=7854, 24 heads: QK-RMSNorm + RoPE + fp32 "
+                  f"torch SDPA, oracle/ref.py), median of {c['reps']} run(s), {c['ms'] / 1e3:.2f} s each; "
+                  f"fp32 and bf16 for configs A, B, C under 'table'",
+        "table": table,
     }
 
 
@@ -274,12 +327,14 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=25.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-dit", action="store_true", help="skip the block (D) and 30-layer DiT (E) runs")
     ap.add_argument("--dit-steps", type=int, default=10)
     ap.add_argument("--dit-layers", type=int, default=30)
+    ap.add_argument("--profile-config", choices=["A", "B", "C"], default=None,
+                    help="only run the timed steps of one attention config (for rocprofv3 counters)")
     ap.add_argument("--profile-copy", type=int, default=0, metavar="BYTES",
                     help="only run 10 device-to-device copies of BYTES (HBM counter calibration)")
     args = ap.parse_args()
@@ -305,6 +360,16 @@ def main():
         torch.cuda.synchronize()
         log(f"copied {src.numel() * 4} bytes 10 times")
         return
+    if args.profile_config:
+        if args.profile_config == "B":
+            r, _ = bench_cross(torch, W, dev, args.steps, args.warmup)
+            log(f"config B: attention kernel {r['attn_kernel_ms']:.4f} ms")
+        else:
+            t, _ = make_inputs(torch, GRID_C if args.profile_config == "C" else GRID_A, 0, dev)
+            fs = FusedSelf(torch, W, t)
+            total, (_, t_attn) = time_steps(torch, [fs.prep, fs.attn], args.steps, args.warmup)
+            log(f"config {args.profile_config}: attention kernel {t_attn:.4f} ms")
+        return
     props = torch.cuda.get_device_properties(dev)
     log(f"device {props.name} {getattr(props, 'gcnArchName', '')} CUs={props.multi_processor_count}")
 
@@ -320,7 +385,7 @@ def main():
 
     extra = {}
     if not args.no_extra:
-        tA, _ = make_inputs(torch, GRID_A, 1, dev)
+        tA, hostA = make_inputs(torch, GRID_A, 1, dev)
         fA = FusedSelf(torch, W, tA)
         totA, (pA, aA) = time_steps(torch, [fA.prep, fA.attn], args.steps, args.warmup)
         LA = tA["q"].shape[1]
@@ -329,7 +394,7 @@ def main():
             "ms_per_step": totA / args.steps, "attn_kernel_ms": aA, "prep_ms": pA,
             "tflops_step": attn_flops(B, H, LA, LA) / (totA / args.steps * 1e-3) / 1e12,
             "tflops_kernel": attn_flops(B, H, LA, LA) / (aA * 1e-3) / 1e12}
-        extra["cross_attn"] = bench_cross(torch, W, dev, args.steps, args.warmup)
+        extra["cross_attn"], hostB = bench_cross(torch, W, dev, args.steps, args.warmup)
         extra.update(bench_torch_sdpa(torch, t, min(args.steps, 20), 3))
         log(f"extra: {json.dumps(extra)}")
     if not args.no_dit:
@@ -338,9 +403,19 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(torch, host, args.cpu_seconds)
-        log(f"cpu baseline: {cpu}")
+        host["flops"] = flops
+        host["workload"] = f"self-attn B=2 L={L} (grid 21x17x22)"
+        hosts = {"C": host}
+        if not args.no_extra:
+            LA = hostA["q"].shape[1]
+            hostA.update(flops=attn_flops(B, H, LA, LA), workload=f"self-attn B=2 L={LA} (grid 6x12x15)")
+            hosts.update(A=hostA, B=hostB)
+        else:
+            hosts.update(A=None, B=None)
+        cpu = cpu_baseline(torch, {k: v for k, v in hosts.items()}, args.cpu_seconds)
+        log(f"cpu baseline: {json.dumps(cpu)}")
 
+    traffic, traffic_note = profiled_traffic()
     line = {
         "metric": "self-attn TFLOP/s @L=7854 (% bf16 MFMA peak); DiT s/step 704x544x81",
         "value": flops / (ms * 1e-3) / 1e12,
@@ -359,8 +434,8 @@ def main():
                    "global_batch": B, "seq_len": L, "heads": H, "head_dim": D, "parallelism": "none (1 GPU)"},
         "roofline": {"kernel": "flash_fwd_kernel<8,2> (attention with the Q RMSNorm + RoPE applied in-kernel)",
                      "bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS, "traffic": profiled_traffic(),
-                     "traffic_source": TRAFFIC_PROFILE + " (FETCH_SIZE x2.0 + WRITE_SIZE x1.0, per launch)",
+                     "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic,
+                     "traffic_source": traffic_note, "kernel_source_sha256": kernel_source_hash(),
                      "kernel_ms": t_attn, "flops_per_launch": flops},
         "cpu_baseline": cpu,
         "prep_ms": t_prep,
