@@ -16,7 +16,8 @@ attention, on seeded N(0,1) projections already resident in HBM.
               median of up to 3 runs; configs A and B and bf16 under "table"
   extra       the same path at L=1080 and the masked cross-attention (Lq=7854,
               512 text keys, per-sample lengths U[16, 512]), with HBM GB/s; torch's
-              own flash SDPA on the config C shapes, for comparison; one
+              own flash SDPA on the config C shapes, for comparison; the q/k/v
+              projection + QK-RMSNorm prep by hipBLASLt and by the sums-of-squares GEMM; one
               WanAttentionBlock (D) and the 30-layer DiT, 10 UniPC steps (E):
               dit_s_per_step is the second half of the metric
 
@@ -185,6 +186,56 @@ def bench_cross(torch, W, dev, steps, warmup):
         "hbm_gbs_kernel": byts / (t_attn * 1e-3) / 1e9,
         "frac_hbm_peak": byts / (t_attn * 1e-3) / 1e9 / PEAK_HBM_GBS,
     }, host
+
+
+def bench_qkv(torch, W, dev, steps, warmup):
+    """The block's q/k/v projection and QK-RMSNorm prep at config C (x [2, 7854, 3072],
+    concatenated weight [9216, 3072]) by the two routes: hipBLASLt's GEMM, then
+    wan_rms_norm_qk (q statistics + k norm/rope from the rows); or wan_qkv_proj_sumsq, the
+    gfx950 GEMM that emits the sums of squares, then wan_rms_norm_qk_sumsq (no q read)."""
+    import torch.nn.functional as F
+    N_, lib = W._native, W._native.lib()
+    L = GRID_C[0] * GRID_C[1] * GRID_C[2]
+    C = H * D
+    g = torch.Generator(device=dev).manual_seed(21)
+    x = torch.randn(B, L, C, device=dev, generator=g).to(torch.bfloat16)
+    w = (torch.randn(3 * C, C, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    bias = (torch.randn(3 * C, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    gk = (1 + torch.rand(C, device=dev, generator=g)).to(torch.bfloat16)
+    cos, sin = (t.to(dev) for t in W.rope.rope_tables(W.rope.wan_freqs(D), GRID_C, D))
+    qkv = torch.empty(B, L, 3 * C, device=dev, dtype=torch.bfloat16)
+    ss = torch.empty(4 * H, B * L, device=dev, dtype=torch.float32)
+    inv = torch.empty(B * L, device=dev, dtype=torch.float32)
+    khat = torch.empty(B, L, H, D, device=dev, dtype=torch.bfloat16)
+    s = torch.cuda.current_stream().cuda_stream
+    q = qkv[..., :C].view(B, L, H, D)
+    k = qkv[..., C:2 * C].view(B, L, H, D)
+
+    def gemm_blas():
+        F.linear(x, w, bias)         # as the block calls it
+
+    def prep_rows():
+        N_.check("qk prep", lib.wan_rms_norm_qk(N_.tensor4(q), N_.tensor4(k), khat.data_ptr(), B, L, H, D,
+                                                gk.data_ptr(), 1e-6, cos.data_ptr(), sin.data_ptr(),
+                                                inv.data_ptr(), s))
+
+    def gemm_sumsq():
+        N_.check("qkv gemm", lib.wan_qkv_proj_sumsq(x.data_ptr(), w.data_ptr(), bias.data_ptr(), qkv.data_ptr(),
+                                                    ss.data_ptr(), B * L, 3 * C, C, C, C, 3 * C, 2 * C, s))
+
+    def prep_sums():
+        N_.check("qk prep from sums", lib.wan_rms_norm_qk_sumsq(N_.tensor4(k), khat.data_ptr(), B, L, H, D,
+                                                                gk.data_ptr(), 1e-6, cos.data_ptr(), sin.data_ptr(),
+                                                                ss.data_ptr(), inv.data_ptr(), s))
+    # the two routes interleaved in the same steps (prep_rows reads the q/k the sums GEMM wrote)
+    _, (t_gemm, t_sums, t_blas, t_rows) = time_steps(torch, [gemm_sumsq, prep_sums, gemm_blas, prep_rows],
+                                                      steps, warmup)
+    flops = 2.0 * B * L * 3 * C * C
+    return {"qkv_projection": {
+        "workload": f"x [2, {L}, 3072] x [9216, 3072]^T + bias, then the QK-RMSNorm prep of the fused self-attention",
+        "hipblaslt_gemm_ms": t_blas, "prep_from_rows_ms": t_rows, "hipblaslt_route_ms": t_blas + t_rows,
+        "sumsq_gemm_ms": t_gemm, "prep_from_sums_ms": t_sums, "sumsq_route_ms": t_gemm + t_sums,
+        "hipblaslt_tflops": flops / (t_blas * 1e-3) / 1e12, "sumsq_gemm_tflops": flops / (t_gemm * 1e-3) / 1e12}}
 
 
 def bench_torch_sdpa(torch, t, steps, warmup):
@@ -396,6 +447,7 @@ def main():
             "tflops_kernel": attn_flops(B, H, LA, LA) / (aA * 1e-3) / 1e12}
         extra["cross_attn"], hostB = bench_cross(torch, W, dev, args.steps, args.warmup)
         extra.update(bench_torch_sdpa(torch, t, min(args.steps, 20), 3))
+        extra.update(bench_qkv(torch, W, dev, min(args.steps, 20), 3))
         log(f"extra: {json.dumps(extra)}")
     if not args.no_dit:
         extra.update(bench_dit(torch, W, dev, args.dit_steps, args.dit_layers))

@@ -159,6 +159,17 @@ int wan_rms_norm_qk(wan_tensor q, wan_tensor k, void* k_out, int batch, int seql
                     const float* rope_sin, float* inv_rms_q, void* stream);
 
 /*
+ * wan_rms_norm_qk with the sums of squares taken from wan_qkv_proj_sumsq instead of the
+ * rows (models/fast_dit.py:134-147 with the statistics from the projection's epilogue):
+ * sumsq fp32 [4 * heads, B * L], the GEMM's 64-column partials of q (rows 0 .. 2 heads - 1)
+ * and k (2 heads .. 4 heads - 1) for every token (GEMM row b * L + l).  Writes inv_rms_q
+ * (fp32 [B*L]) without reading q, and k_out = rope(bf16(bf16(k * inv_rms_k) * gamma_k)).
+ */
+int wan_rms_norm_qk_sumsq(wan_tensor k, void* k_out, int batch, int seqlen, int heads, int head_dim,
+                          const void* gamma_k, float eps, const float* rope_cos, const float* rope_sin,
+                          const float* sumsq, float* inv_rms_q, void* stream);
+
+/*
  * Attention whose query is normalised inside the kernel as it is loaded:
  *   q' = rope?(bf16(bf16(q * inv_rms_q[b, i]) * gamma_q)),  out = softmax(q' k^T * scale) v
  * with inv_rms_q from wan_rms_norm (fp32 [B*Lq]).  rope_cos/rope_sin NULL: no
@@ -192,6 +203,21 @@ int wan_flash_attn_qnorm(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor ou
 int wan_adaln(const void* x, const void* y, void* x_out, void* h_out, int batch, int seqlen,
               int dim, const void* e, int frames, int gate_idx, int shift_idx, int scale_idx,
               const void* ln_weight, const void* ln_bias, float eps, void* stream);
+
+/*
+ * The block's q/k/v projection with the statistics of the QK-RMSNorm in its epilogue:
+ *   out[m, n]   = bf16(sum_k x[m, k] w[n, k] + bias[n])           (bf16, fp32 accumulation)
+ *   sumsq[p, m] = sum over columns 64 p .. 64 p + 63 of bf16(out[m, n])^2,  p < sq_cols / 64
+ * x [M, K] (row stride ldx), w [N, K] (ldw; an nn.Linear weight: the concatenated q, k, v
+ * weights), bias [N], out [M, N] (ldo), sumsq fp32 [sq_cols / 64, M].  Replaces
+ * _lin(h, sa.q), _lin(h, sa.k), _lin(h, sa.v) of models/fast_dit.py:281-282 together with
+ * the per-token sums of squares of _tp_rms_qk (:134-147): with sq_cols = 2 * heads * 128
+ * the q and k sums of every head come out of the GEMM and wan_self_attn_fused_sumsq needs
+ * no q statistics pass.  N must be a multiple of 256, K of 64, sq_cols of 64.
+ */
+int wan_qkv_proj_sumsq(const void* x, const void* w, const void* bias, void* out, float* sumsq,
+                       int M, int N, int K, int64_t ldx, int64_t ldw, int64_t ldo, int sq_cols,
+                       void* stream);
 
 #ifdef __cplusplus
 }

@@ -29,6 +29,7 @@ _P = ctypes.c_void_p
 _I = ctypes.c_int
 _F = ctypes.c_float
 _SZ = ctypes.c_size_t
+_L = ctypes.c_int64
 _T = WanTensor
 
 # name -> (restype, argtypes), one entry per function in include/wan_attn.h
@@ -47,6 +48,8 @@ SIGNATURES = {
     "wan_rms_norm_qk": (_I, [_T, _T, _P, _I, _I, _I, _I, _P, _F, _P, _P, _P, _P]),
     "wan_flash_attn_qnorm": (_I, [_T, _T, _T, _T, _I, _I, _I, _I, _I, _P, _P, _P, _P, _F, _P, _P]),
     "wan_adaln": (_I, [_P, _P, _P, _P, _I, _I, _I, _P, _I, _I, _I, _I, _P, _P, _F, _P]),
+    "wan_qkv_proj_sumsq": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _L, _L, _L, _I, _P]),
+    "wan_rms_norm_qk_sumsq": (_I, [_T, _P, _I, _I, _I, _I, _P, _F, _P, _P, _P, _P, _P]),
 }
 
 ABI_VERSION = 1

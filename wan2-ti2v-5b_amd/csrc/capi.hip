@@ -212,6 +212,33 @@ int wan_rms_norm_qk(wan_tensor q, wan_tensor k, void* k_out, int batch, int seql
   return launch_rms_prep2(aq, ak, static_cast<hipStream_t>(stream));
 }
 
+int wan_rms_norm_qk_sumsq(wan_tensor k, void* k_out, int batch, int seqlen, int heads, int head_dim,
+                          const void* gamma_k, float eps, const float* rope_cos, const float* rope_sin,
+                          const float* sumsq, float* inv_rms_q, void* stream) {
+  const char* fn = "wan_rms_norm_qk_sumsq";
+  if (inv_rms_q == nullptr || k_out == nullptr || sumsq == nullptr)
+    return set_error(WAN_ERR_INVALID, "%s: sumsq, inv_rms_q and k_out are required", fn);
+  if (!aligned16(sumsq)) return set_error(WAN_ERR_INVALID, "%s: sumsq must be 16-byte aligned", fn);
+  if (heads * 2 > 64)
+    return set_error(WAN_ERR_UNSUPPORTED, "%s: %d heads give %d partial sums per token, at most 64", fn,
+                     heads, heads * 2);
+  PrepArgs aq{}, ak{};
+  int rc;
+  // q: statistics only, no x read (any valid tensor satisfies the checks)
+  if ((rc = rms_prep_args(fn, k, nullptr, batch, seqlen, heads, head_dim, nullptr, eps, nullptr,
+                          nullptr, inv_rms_q, &aq)))
+    return rc;
+  if ((rc = rms_prep_args(fn, k, k_out, batch, seqlen, heads, head_dim, gamma_k, eps, rope_cos,
+                          rope_sin, nullptr, &ak)))
+    return rc;
+  if ((int64_t)batch * seqlen * heads == 0) return WAN_OK;
+  aq.sumsq = ak.sumsq = sumsq;
+  aq.sumsq_parts = ak.sumsq_parts = heads * 2;
+  aq.sumsq_first = 0;
+  ak.sumsq_first = heads * 2;
+  return launch_rms_prep2(aq, ak, static_cast<hipStream_t>(stream));
+}
+
 int wan_flash_attn_qnorm(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor out, int batch,
                          int heads, int seqlen_q, int seqlen_k, int head_dim,
                          const float* inv_rms_q, const void* gamma_q, const float* rope_cos,
@@ -428,6 +455,42 @@ int wan_rope(wan_tensor x, void* out, int batch, int seqlen, int heads, int head
   a.sin = rope_sin;
   a.out = static_cast<bf16*>(out);
   return launch_rope(a, static_cast<hipStream_t>(stream));
+}
+
+int wan_qkv_proj_sumsq(const void* x, const void* w, const void* bias, void* out, float* sumsq,
+                       int M, int N, int K, int64_t ldx, int64_t ldw, int64_t ldo, int sq_cols,
+                       void* stream) {
+  const char* fn = "wan_qkv_proj_sumsq";
+  if (M < 0 || N <= 0 || K <= 0)
+    return set_error(WAN_ERR_INVALID, "%s: bad sizes (M=%d N=%d K=%d)", fn, M, N, K);
+  if (N % 256 != 0 || K % 64 != 0)
+    return set_error(WAN_ERR_UNSUPPORTED, "%s: N=%d must be a multiple of 256 and K=%d of 64", fn, N, K);
+  if (sq_cols < 0 || sq_cols % 64 != 0 || sq_cols > N)
+    return set_error(WAN_ERR_INVALID, "%s: sq_cols=%d must be a multiple of 64 in [0, N]", fn, sq_cols);
+  if (ldx < K || ldw < K || ldo < N || ldx % 8 || ldw % 8 || ldo % 8)
+    return set_error(WAN_ERR_INVALID, "%s: row strides (%lld, %lld, %lld) must cover the rows and be "
+                     "multiples of 8 elements", fn, (long long)ldx, (long long)ldw, (long long)ldo);
+  // a tile's 256 rows are addressed with 32-bit byte offsets
+  if (ldx >= (int64_t(1) << 23) || ldw >= (int64_t(1) << 23))
+    return set_error(WAN_ERR_UNSUPPORTED, "%s: row strides must be below 2^23 elements", fn);
+  const void* ptrs[] = {x, w, bias, out, sumsq};
+  for (const void* p : ptrs)
+    if (!aligned16(p) || (p == nullptr && !(p == sumsq && sq_cols == 0) && M > 0))
+      return set_error(WAN_ERR_INVALID, "%s: operands must be 16-byte aligned device pointers", fn);
+  GemmArgs a;
+  a.x = static_cast<const bf16*>(x);
+  a.w = static_cast<const bf16*>(w);
+  a.bias = static_cast<const bf16*>(bias);
+  a.out = static_cast<bf16*>(out);
+  a.sumsq = sumsq;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.ldx = ldx;
+  a.ldw = ldw;
+  a.ldo = ldo;
+  a.sq_cols = sq_cols;
+  return launch_gemm_rowsq(a, static_cast<hipStream_t>(stream));
 }
 
 int wan_adaln(const void* x, const void* y, void* x_out, void* h_out, int batch, int seqlen,

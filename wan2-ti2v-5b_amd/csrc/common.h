@@ -62,6 +62,10 @@ struct PrepArgs {
   const float* cos;     // [L, 64] fp32 (null: no rotation)
   const float* sin;
   bf16* out;            // out [B, L, H, 128] contiguous (null: statistics only)
+  // Sums of squares given by the projection GEMM instead of computed from x:
+  // partials sumsq[(sumsq_first + p) * B * L + token], p < sumsq_parts (null: from x).
+  const float* sumsq;
+  int sumsq_first, sumsq_parts;
 };
 int launch_rms_prep(const PrepArgs& a, hipStream_t s);
 // Two tasks with the same H in one launch.
@@ -110,5 +114,18 @@ struct FlashArgs {
   const float* sin;
 };
 int launch_flash_fwd(const FlashArgs& a, hipStream_t s);
+
+// out = bf16(x w^T + bias) with per-head sums of squares of the first sq_cols columns.
+struct GemmArgs {
+  const bf16* x;        // [M, K] (row stride ldx)
+  const bf16* w;        // [N, K] (row stride ldw), an nn.Linear weight
+  const bf16* bias;     // [N]
+  bf16* out;            // [M, N] (row stride ldo)
+  float* sumsq;         // [sq_cols / 64, M]: per 64 columns, sum of bf16(out)^2
+  int M, N, K;
+  int64_t ldx, ldw, ldo;
+  int sq_cols;          // multiple of 64, <= N
+};
+int launch_gemm_rowsq(const GemmArgs& a, hipStream_t s);
 
 }  // namespace wan

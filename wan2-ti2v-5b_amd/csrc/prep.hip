@@ -47,16 +47,29 @@ __device__ __forceinline__ void rms_prep_rows(const PrepArgs& a, int block) {
 
   bf16x8 xv[NCH];
   float ss = 0.f;
+  if (a.sumsq != nullptr) {
+    // the projection GEMM's partial sums (one per lane, then the wave's sum); the row
+    // itself is read only when the normalised row is wanted
+    if (lane < a.sumsq_parts) ss = a.sumsq[(int64_t)(a.sumsq_first + lane) * (a.B * a.L) + tok];
+    if (a.out != nullptr) {
 #pragma unroll
-  for (int i = 0; i < NCH; ++i) {
-    const int c = lane + 64 * i;
-    if (c < nchunks) {
-      const int h = c >> 4, d0 = (c & 15) * 8;
-      xv[i] = *reinterpret_cast<const bf16x8*>(row + h * a.x.sh + d0);
+      for (int i = 0; i < NCH; ++i) {
+        const int c = lane + 64 * i;
+        if (c < nchunks) xv[i] = *reinterpret_cast<const bf16x8*>(row + (c >> 4) * a.x.sh + (c & 15) * 8);
+      }
+    }
+  } else {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float f = (float)xv[i][j];
-        ss += f * f;
+    for (int i = 0; i < NCH; ++i) {
+      const int c = lane + 64 * i;
+      if (c < nchunks) {
+        const int h = c >> 4, d0 = (c & 15) * 8;
+        xv[i] = *reinterpret_cast<const bf16x8*>(row + h * a.x.sh + d0);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float f = (float)xv[i][j];
+          ss += f * f;
+        }
       }
     }
   }

@@ -11,6 +11,8 @@ chosen once at import, under the reference's selector names (models/fast_dit.py:
                        Q-RMSNorm + masked cross-attention kernel (ops.cross_attn_fused)
   FAST_POINTWISE_IMPL  "hip" (default): each pointwise stage of a block is one fused pass
                        (ops.adaln) and GELU is the FFN-up GEMM's epilogue; "eager": torch ops
+  FAST_QKV_IMPL        with "hip" attention, the q/k/v projection: "hipblaslt" (default) or
+                       "hip", the gfx950 GEMM that also emits the QK-RMSNorm sums of squares
 
 A block (models/fast_dit.py:270-311) is organised here as four pointwise stages between
 its GEMM groups, e the block's per-frame modulation rows:
@@ -41,12 +43,19 @@ from .model import WanModel, sinusoidal_embedding_1d
 FAST_ATTN_IMPL = os.environ.get("FAST_ATTN_IMPL", "hip")
 FAST_CROSS_IMPL = os.environ.get("FAST_CROSS_IMPL", FAST_ATTN_IMPL)
 FAST_POINTWISE_IMPL = os.environ.get("FAST_POINTWISE_IMPL", "hip")
+# The fused q/k/v projection of the "hip" self-attention: "hipblaslt" (default), or "hip", the
+# gfx950 GEMM whose epilogue emits the QK-RMSNorm sums of squares (ops.qkv_proj_sumsq), so the
+# q statistics pass disappears; it measures 0.72 ms against hipBLASLt's 0.61 ms at the
+# config C shape, more than the 19 us the pass costs, hence not the default.
+FAST_QKV_IMPL = os.environ.get("FAST_QKV_IMPL", "hipblaslt")
 IMPLS = ("hip", "sdpa")
 for _name, _val in (("FAST_ATTN_IMPL", FAST_ATTN_IMPL), ("FAST_CROSS_IMPL", FAST_CROSS_IMPL)):
     if _val not in IMPLS:
         raise ValueError(f"{_name}={_val!r}: expected one of {IMPLS}")
 if FAST_POINTWISE_IMPL not in ("hip", "eager"):
     raise ValueError(f"FAST_POINTWISE_IMPL={FAST_POINTWISE_IMPL!r}: expected 'hip' or 'eager'")
+if FAST_QKV_IMPL not in ("hipblaslt", "hip"):
+    raise ValueError(f"FAST_QKV_IMPL={FAST_QKV_IMPL!r}: expected 'hipblaslt' or 'hip'")
 
 
 def _linear(x, layer):
@@ -142,12 +151,14 @@ class _FastBlock:
     at TP=1, as the four stages of the module docstring."""
 
     def __init__(self, block, num_frames: int, attn_impl: str = FAST_ATTN_IMPL,
-                 cross_impl: str = FAST_CROSS_IMPL, pointwise_impl: str = FAST_POINTWISE_IMPL):
+                 cross_impl: str = FAST_CROSS_IMPL, pointwise_impl: str = FAST_POINTWISE_IMPL,
+                 qkv_impl: str = FAST_QKV_IMPL):
         self.block = block
         self.num_frames = num_frames
         self.attn_impl = attn_impl
         self.cross_impl = cross_impl
         self.pointwise_impl = pointwise_impl
+        self.qkv_impl = qkv_impl
         sa = block.self_attn
         if attn_impl == "hip":
             self.w_qkv = torch.cat([sa.q.weight, sa.k.weight, sa.v.weight], 0).contiguous()
@@ -178,6 +189,11 @@ class _FastBlock:
         heads = (B, L, sa.num_heads, sa.head_dim)
         scale = sa.head_dim ** -0.5
         if self.attn_impl == "hip":
+            if self.qkv_impl == "hip":
+                qkv, sumsq = ops.qkv_proj_sumsq(h.contiguous(), self.w_qkv, self.b_qkv, 2 * C)
+                q, k, v = (t.view(heads) for t in qkv.split(C, dim=-1))
+                return ops.self_attn_fused_sumsq(q, k, v, sumsq, sa.norm_q.weight, sa.norm_k.weight,
+                                                 sa.norm_q.eps, cos, sin, scale)
             q, k, v = (t.view(heads) for t in F.linear(h, self.w_qkv, self.b_qkv).split(C, dim=-1))
             return ops.self_attn_fused(q, k, v, sa.norm_q.weight, sa.norm_k.weight, sa.norm_q.eps,
                                        cos, sin, scale)

@@ -347,3 +347,72 @@ def adaln(x: torch.Tensor, y: Optional[torch.Tensor] = None, e: Optional[torch.T
     Returns (r, h); h is None when norm is False."""
     r, h = adaln_stage(x, y, e, frames, gate_idx, shift_idx, scale_idx, ln_weight, ln_bias, eps, norm)
     return (x if y is None else r), (h if norm else None)
+
+
+# ─── the q/k/v projection with the QK-RMSNorm statistics in its epilogue ───────
+
+@torch.library.custom_op("wan_hip::qkv_proj_sumsq", mutates_args=())
+def qkv_proj_sumsq(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor,
+                   sq_cols: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """out = bf16(x weight^T + bias) for x [B, L, C] and an nn.Linear weight [N, C], with
+    sumsq [sq_cols / 64, B * L] fp32: each token's sum of squares of bf16(out) over every
+    64 of the first sq_cols columns (wan_qkv_proj_sumsq)."""
+    fn = "qkv_proj_sumsq"
+    if x.dim() != 3:
+        raise ValueError(f"{fn}: x must be [B, L, C], got {tuple(x.shape)}")
+    B, L, C = x.shape
+    Nn = weight.shape[0]
+    _check_rows(fn, "x", x, (B, L, C), x.device)
+    _check_rows(fn, "weight", weight, (Nn, C), x.device)
+    _check_rows(fn, "bias", bias, (Nn,), x.device)
+    out = torch.empty((B, L, Nn), dtype=x.dtype, device=x.device)
+    sumsq = torch.empty((max(sq_cols // 64, 1), B * L), dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        N.check("wan_qkv_proj_sumsq", N.lib().wan_qkv_proj_sumsq(
+            x.data_ptr(), weight.data_ptr(), bias.data_ptr(), out.data_ptr(), sumsq.data_ptr(),
+            B * L, Nn, C, C, C, Nn, int(sq_cols), _stream(x.device)))
+    return out, sumsq
+
+
+@qkv_proj_sumsq.register_fake
+def _(x, weight, bias, sq_cols):
+    B, L, _ = x.shape
+    return (x.new_empty((B, L, weight.shape[0])),
+            x.new_empty((max(sq_cols // 64, 1), B * L), dtype=torch.float32))
+
+
+@torch.library.custom_op("wan_hip::self_attn_fused_sumsq", mutates_args=())
+def self_attn_fused_sumsq(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, sumsq: torch.Tensor,
+                          gamma_q: torch.Tensor, gamma_k: torch.Tensor, eps: float,
+                          cos: torch.Tensor, sin: torch.Tensor, softmax_scale: float) -> torch.Tensor:
+    """self_attn_fused with the QK-RMSNorm statistics from qkv_proj_sumsq (sumsq
+    [4 H, B L]: q's 64-column partials, then k's): the q statistics pass disappears and
+    the k pass reads k only to normalise and rotate it (wan_rms_norm_qk_sumsq)."""
+    fn = "self_attn_fused_sumsq"
+    _check_qkv(fn, q, k, v)
+    B, L, H, D = q.shape
+    if k.shape[1] != L:
+        raise ValueError(f"{fn}: self-attention needs Lq == Lk, got {L} and {k.shape[1]}")
+    _check_vec(fn, "gamma_q", gamma_q, H * D, torch.bfloat16, q.device)
+    _check_vec(fn, "gamma_k", gamma_k, H * D, torch.bfloat16, q.device)
+    _check_vec(fn, "sumsq", sumsq, 4 * H * B * L, torch.float32, q.device)
+    _check_rope(fn, cos, sin, L, q.device)
+    lib = N.lib()
+    inv = torch.empty(B * L, dtype=torch.float32, device=q.device)
+    khat = torch.empty((B, L, H, D), dtype=q.dtype, device=q.device)
+    out = torch.empty((B, L, H, D), dtype=q.dtype, device=q.device)
+    s = _stream(q.device)
+    with torch.cuda.device(q.device):
+        N.check("wan_rms_norm_qk_sumsq", lib.wan_rms_norm_qk_sumsq(
+            N.tensor4(k), khat.data_ptr(), B, L, H, D, gamma_k.data_ptr(), float(eps),
+            cos.data_ptr(), sin.data_ptr(), sumsq.data_ptr(), inv.data_ptr(), s))
+        N.check("wan_flash_attn_qnorm", lib.wan_flash_attn_qnorm(
+            N.tensor4(q), N.tensor4(khat), N.tensor4(v), N.tensor4(out), B, H, L, L, D,
+            inv.data_ptr(), gamma_q.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+            float(softmax_scale), None, s))
+    return out
+
+
+@self_attn_fused_sumsq.register_fake
+def _(q, k, v, sumsq, gamma_q, gamma_k, eps, cos, sin, softmax_scale):
+    return q.new_empty(q.shape)
