@@ -13,15 +13,24 @@
 // The MFMA computes out^T tiles, w rows on the MFMA row axis and x rows on the column
 // axis, so a lane holds one output row (lane % 32) and half of each 64-column block: a
 // 64-column sum of squares is lane-local plus one exchange with the lane 32 apart, as
-// the attention kernel's softmax row sums are.  K advances 64 per step; the 256 x 64
+// the attention kernel's softmax row sums are.  K advances 64 per tile; the 256 x 64
 // tiles of x and w (32 KB each) go global -> LDS by 16-byte copies into rows of eight
 // 16-byte chunks, chunk c of row r at position c ^ ((r / 2) % 8) (conflict-free operand
-// reads), double-buffered, one barrier per step; operand fragments are read one k-step
-// ahead of their MFMAs.  Workgroups run in groups of 8 M-tiles per N-tile, each XCD
-// owning a contiguous range, so the tiles running together on an XCD share x and w
-// rows in its L2.  At the QKV shape (M 15708, N 9216, K 3072) it reaches 1.12-1.24
-// PFLOP/s, 83-86% of hipBLASLt's F.linear timed beside it, with output bit-identical.
+// reads), in two slots, one barrier per tile.  Program order is pinned MFMA by MFMA:
+// each MFMA is followed by one fragment read of the next k-step and, in a tile's first
+// k-step, one copy of the next tile, and the barrier sits inside the last k-step so the
+// next tile's first reads overlap its remaining MFMAs.  Workgroups run in groups of 8
+// M-tiles per N-tile, each XCD owning a contiguous range, so the tiles running together
+// on an XCD share x and w rows in its L2.
+//
+// At the QKV shape (M 15708, N 9216, K 3072) it reaches 1.20-1.27 PFLOP/s, 84-86% of
+// hipBLASLt's F.linear timed beside it, with output bit-identical.  Both are power
+// limited (all-zero operands run either ~25% faster); on zeros this kernel's k-loop is
+// ~13% slower per tile than hipBLASLt's, and 4 waves of 128 x 128 (a third less LDS
+// read traffic, one wave per SIMD) measured slower than this tiling.
 #include "common.h"
+
+#include <type_traits>
 
 namespace wan {
 
@@ -88,7 +97,10 @@ struct GemmTileLoader {
   }
   __device__ __forceinline__ void issue(const char* tile_base, bf16* dst, int wave) const {
 #pragma unroll
-    for (int i = 0; i < C::kPerWave; ++i) dma16(tile_base, off[i], lds_addr(dst + (wave + C::kWaves * i) * 512));
+    for (int i = 0; i < C::kPerWave; ++i) issue_one(tile_base, dst, wave, i);
+  }
+  __device__ __forceinline__ void issue_one(const char* tile_base, bf16* dst, int wave, int i) const {
+    dma16(tile_base, off[i], lds_addr(dst + (wave + C::kWaves * i) * 512));
   }
 };
 
@@ -136,47 +148,72 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_rowsq_kernel(const GemmA
     for (int j = 0; j < C::TM; ++j) acc[i][j] = f32x16{};
 
   const int kt_count = a.K / BK;
-  auto issue_stage = [&](int kt) {
-    const int64_t kb = (int64_t)kt * BK * 2;
-    xl.issue(xbase + kb, xs[kt & 1], wave);
-    wl.issue(wbase + kb, ws[kt & 1], wave);
-  };
-  auto frags = [&](int kt, int ks, bf16x8 wf[C::TN], bf16x8 xf[C::TM]) {
-    const bf16* X = xs[kt & 1];
-    const bf16* Wt = ws[kt & 1];
+  auto read_frag = [&](int slot, int ks, int i, bf16x8 wf[C::TN], bf16x8 xf[C::TM]) {
     const int pos = ((2 * ks + hh) ^ sw) << 3;
-#pragma unroll
-    for (int b = 0; b < C::TN; ++b) wf[b] = *reinterpret_cast<const bf16x8*>(Wt + wrow[b] * BK + pos);
-#pragma unroll
-    for (int b = 0; b < C::TM; ++b) xf[b] = *reinterpret_cast<const bf16x8*>(X + xrow[b] * BK + pos);
+    if (i < C::TN)
+      wf[i] = *reinterpret_cast<const bf16x8*>(ws[slot] + wrow[i] * BK + pos);
+    else
+      xf[i - C::TN] = *reinterpret_cast<const bf16x8*>(xs[slot] + xrow[i - C::TN] * BK + pos);
   };
-  constexpr int KS = BK / 16;          // MFMA k-steps per stage
+  auto copy_one = [&](int slot, int kt, int i) {
+    const int64_t kb = (int64_t)kt * BK * 2;
+    if (i < C::kPerWave)
+      xl.issue_one(xbase + kb, xs[slot], wave, i);
+    else
+      wl.issue_one(wbase + kb, ws[slot], wave, i - C::kPerWave);
+  };
+  constexpr int KS = BK / 16;             // MFMA k-steps per tile
+  constexpr int NF = C::TN + C::TM;       // fragment reads per k-step
+  constexpr int NM = C::TN * C::TM;       // MFMAs per k-step
+  constexpr int NC = 2 * C::kPerWave;     // copies per tile and wave
+  constexpr int SPLIT = NM - NF;          // MFMAs of the last k-step before the barrier
+  static_assert(KS % 2 == 0 && NF <= NM, "schedule");
 
-  // Two stages: step kt computes stage kt while stage kt + 1 is copied into the other
-  // buffer; one barrier per step publishes the copy and retires the stage.
-  issue_stage(0);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  for (int kt = 0; kt < kt_count; ++kt) {
-    if (kt + 1 < kt_count) issue_stage(kt + 1);
-    bf16x8 wf[2][C::TN], xf[2][C::TM];
-    frags(kt, 0, wf[0], xf[0]);
+  bf16x8 wf[2][C::TN], xf[2][C::TM];
+
+  // One tile of k.  Program order is fixed MFMA by MFMA (a scheduling barrier after
+  // each): after MFMA m of k-step ks comes fragment read m of k-step ks + 1 (the reads
+  // are in flight behind the MFMAs that follow) and, in k-step 0, copy m of the next
+  // tile into the other slot.  The last k-step splits around the barrier that publishes
+  // the next tile: NM - NF MFMAs, the copies' wait and the barrier, then NF MFMAs, each
+  // followed by a read of the next tile's first k-step.
+  auto tile = [&](int kt, auto has_next_c) {
+    constexpr bool has_next = decltype(has_next_c)::value;
+    const int slot = kt & 1, nslot = slot ^ 1;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int cur = ks & 1, nxt = cur ^ 1;
-      if (ks + 1 < KS) frags(kt, ks + 1, wf[nxt], xf[nxt]);
-      // the reads go out a whole k-step ahead of their MFMAs (left to itself the
-      // compiler moves them down to the MFMAs, to reuse registers, and exposes the
-      // LDS latency every k-step)
-      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int nb = 0; nb < C::TN; ++nb)
+      for (int m = 0; m < NM; ++m) {
+        if (ks == KS - 1 && m == SPLIT) {
+          // every wave's copies of the next tile landed, every read of this slot returned
+          asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        const int nb = m / C::TM, mb = m % C::TM;
+        acc[nb][mb] = mfma32(wf[cur][nb], xf[cur][mb], acc[nb][mb]);
+        if (ks < KS - 1) {
+          if (m < NF) read_frag(slot, ks + 1, m, wf[nxt], xf[nxt]);
+        } else if (has_next && m >= SPLIT) {
+          read_frag(nslot, 0, m - SPLIT, wf[nxt], xf[nxt]);
+        }
+        if (has_next && ks == 0 && m < NC) copy_one(nslot, kt + 1, m);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (has_next && ks == 0) {
 #pragma unroll
-        for (int mb = 0; mb < C::TM; ++mb) acc[nb][mb] = mfma32(wf[cur][nb], xf[cur][mb], acc[nb][mb]);
+        for (int i = NM; i < NC; ++i) copy_one(nslot, kt + 1, i);
+      }
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-  }
+  };
+
+  for (int i = 0; i < NC; ++i) copy_one(0, 0, i);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < NF; ++i) read_frag(0, 0, i, wf[0], xf[0]);
+  for (int kt = 0; kt + 1 < kt_count; ++kt) tile(kt, std::integral_constant<bool, true>{});
+  tile(kt_count - 1, std::integral_constant<bool, false>{});
   __syncthreads();   // every wave is done with the last stage before the output staging
 
   // Epilogue, one 32-row block at a time: bias, bf16 rounding, the sums of squares over
