@@ -23,7 +23,7 @@ attention, on seeded N(0,1) projections already resident in HBM.
 
 Prints one JSON line on stdout.  Usage:
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--cpu-seconds S] [--no-cpu-baseline]
-  python bench.py --profile-config {A,B,C} [--steps K]   (one config's steps only, for rocprofv3)
+  python bench.py --profile-config {A,B,C,QKV} [--steps K]   (one config's steps only, for rocprofv3)
 """
 import argparse
 import json
@@ -384,8 +384,9 @@ def main():
     ap.add_argument("--no-dit", action="store_true", help="skip the block (D) and 30-layer DiT (E) runs")
     ap.add_argument("--dit-steps", type=int, default=10)
     ap.add_argument("--dit-layers", type=int, default=30)
-    ap.add_argument("--profile-config", choices=["A", "B", "C"], default=None,
-                    help="only run the timed steps of one attention config (for rocprofv3 counters)")
+    ap.add_argument("--profile-config", choices=["A", "B", "C", "QKV"], default=None,
+                    help="only run the timed steps of one attention config, or of the two QKV "
+                         "projection routes (for rocprofv3 counters)")
     ap.add_argument("--profile-copy", type=int, default=0, metavar="BYTES",
                     help="only run 10 device-to-device copies of BYTES (HBM counter calibration)")
     args = ap.parse_args()
@@ -415,6 +416,9 @@ def main():
         if args.profile_config == "B":
             r, _ = bench_cross(torch, W, dev, args.steps, args.warmup)
             log(f"config B: attention kernel {r['attn_kernel_ms']:.4f} ms")
+        elif args.profile_config == "QKV":
+            r = bench_qkv(torch, W, dev, args.steps, args.warmup)["qkv_projection"]
+            log(f"QKV projection: gemm {r['sumsq_gemm_ms']:.4f} ms, hipBLASLt {r['hipblaslt_gemm_ms']:.4f} ms")
         else:
             t, _ = make_inputs(torch, GRID_C if args.profile_config == "C" else GRID_A, 0, dev)
             fs = FusedSelf(torch, W, t)
