@@ -284,6 +284,22 @@ def sinusoidal_embedding_1d(dim: int, position: torch.Tensor) -> torch.Tensor:
     return torch.cat([torch.cos(s), torch.sin(s)], dim=1)
 
 
+def text_context(tx, ctx):
+    """The DiT's text embedding `tx` (a Sequential: Linear(text_dim -> dim), tanh-GELU,
+    Linear) in fp32 (wan/modules/model.py:469-475; ref_fp32.py:72-73)."""
+    return _lin32(F.gelu(_lin32(ctx.float(), tx[0]), approximate="tanh"), tx[2])
+
+
+def cross_kv(blk, context, heads, d):
+    """One block's cross-attention keys and values in fp32: K = RMSNorm over all heads of a
+    text token (norm_k), V as projected, each [B, Lc, heads, d] (models/fast_dit.py:464-477)."""
+    ca = blk.cross_attn
+    B = context.shape[0]
+    ck = _rms32(_lin32(context, ca.k), ca.norm_k).view(B, -1, heads, d)
+    cv = _lin32(context, ca.v).view(B, -1, heads, d)
+    return ck, cv
+
+
 def dit_forward(model, latent, t, ctx_cond, ctx_null, grid, guide_scale):
     """CFG noise prediction of the whole DiT in fp32 (ref_fp32.py:62-99): latent [C, F, H, W],
     contexts [1, Lc, text_dim] -> [C_out, F, H, W].
@@ -304,17 +320,13 @@ def dit_forward(model, latent, t, ctx_cond, ctx_null, grid, guide_scale):
     e = _lin32(F.silu(_lin32(s, te[0])), te[2])
     e = e.unsqueeze(0)                                              # [1, F, C]
     e0 = _lin32(F.silu(e), model.time_projection[1]).unflatten(2, (6, dim))
-    tx = model.text_embedding
-    ctx = torch.cat([ctx_cond, ctx_null], 0).float().to(dev)
-    context = _lin32(F.gelu(_lin32(ctx, tx[0]), approximate="tanh"), tx[2])
+    context = text_context(model.text_embedding, torch.cat([ctx_cond, ctx_null], 0).float().to(dev))
     pe = model.patch_embedding
     x = F.conv3d(latent.float().cpu().unsqueeze(0), pe.weight.float().cpu(), pe.bias.float().cpu(),
                  stride=pe.stride).to(dev)
     x = x.flatten(2).transpose(1, 2).expand(2, -1, -1).contiguous()
     for blk in model.blocks:
-        ca = blk.cross_attn
-        ck = _rms32(_lin32(context, ca.k), ca.norm_k).view(2, -1, heads, d)
-        cv = _lin32(context, ca.v).view(2, -1, heads, d)
+        ck, cv = cross_kv(blk, context, heads, d)
         x = block_forward(blk, x, e0, cos, sin, ck, cv, f)
     hd = model.head
     m = [t_.squeeze(2) for t_ in (hd.modulation.float().unsqueeze(0) + e.unsqueeze(2)).chunk(2, dim=2)]

@@ -331,6 +331,39 @@ def test_cross_config_b(W, lens):
     assert ref.rel_rms(out, want) <= 5e-3
 
 
+@pytest.mark.parametrize("lens", ["drawn", (512, 512)])
+def test_cross_config_b_text_recipe(W, lens):
+    """Config B with its K/V built as the pipeline builds them: a [2, 512, 4096] N(0,1) text
+    context through the DiT's text embedding (Linear, tanh-GELU, Linear; std-0.02 weights),
+    then one block's lin_k + RMSNorm and lin_v (models/fast_dit.py:464-477), on the device in
+    bf16 by the product; seqlen_k drawn from U{16..512} (and both 512, the reference
+    pipeline's unmasked case).  K/V against the fp32 chain on the host, then the attention
+    against the fp32 SDPA on the product's own K/V."""
+    import copy
+    B, H, Lq, Lc = 2, 24, 7854, 512
+    m = W.model.random_model(W.model.WanConfig(), num_layers=1, device=DEV, seed=61)
+    blk = m.blocks[0]
+    g = torch.Generator().manual_seed(62)
+    ctx = torch.randn(B, Lc, 4096, generator=g).bfloat16()
+    ck, cv = W.fast_dit.cross_kv(blk, m.text_embedding(ctx.to(DEV)), "hip")
+    host_te = copy.deepcopy(m.text_embedding).float().cpu()
+    host_blk = copy.deepcopy(blk).float().cpu()
+    ck32, cv32 = ref.cross_kv(host_blk, ref.text_context(host_te, ctx), H, D)
+    e_k, e_v = ref.rel_rms(ck.cpu(), ck32), ref.rel_rms(cv.cpu(), cv32)
+    print(f"text recipe: ck {e_k:.2e}, cv {e_v:.2e} from the fp32 chain")
+    assert e_k < 1e-2 and e_v < 1e-2
+    sk = torch.randint(16, Lc + 1, (B,), generator=g, dtype=torch.int32) if lens == "drawn" \
+        else torch.tensor(lens, dtype=torch.int32)
+    q = _bf((B, Lq, H, D), 63)
+    gq = _gammas(H * D, 64, True)
+    out = W.ops.cross_attn_fused(*_d(q), ck, cv, gq.to(DEV), 1e-6, sk.to(DEV), SCALE).cpu()
+    qn = ref.rms(q.reshape(B, Lq, H * D), gq).view(B, Lq, H, D)
+    want = ref.sdpa(qn.float(), ck.cpu().float(), cv.cpu().float(), seqlen_k=sk.tolist())
+    e = ref.rel_rms(out, want)
+    print(f"seqlen_k {sk.tolist()}: attention rel_rms {e:.2e} vs the fp32 SDPA")
+    assert torch.isfinite(out.float()).all() and e <= 5e-3
+
+
 @pytest.mark.parametrize("fused", [False, True])
 def test_persistent_cross_mixed_lengths(W, fused):
     """Per-sample key lengths select the persistent short-key kernel: each workgroup walks
