@@ -128,26 +128,50 @@ class FusedSelf:
 
 
 def time_steps(torch, step_fns, steps, warmup):
-    """Runs `steps` steps of the stage functions; returns (total ms, [ms per stage])."""
+    """Runs `steps` steps of the stage functions; returns (total ms, [ms per stage]).
+
+    The total comes from a pass with events only before the first and after the last step;
+    the per-stage times from a second pass with an event pair around every launch (an event
+    between two kernels delays the second one's dispatch, which the first pass keeps out of
+    the step time)."""
     for _ in range(warmup):
         for f in step_fns:
             f()
     torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        for f in step_fns:
+            f()
+    end.record()
+    torch.cuda.synchronize()
+    total = start.elapsed_time(end)
     n = len(step_fns)
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(n + 1)] for _ in range(steps)]
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
     for s in range(steps):
         ev[s][0].record()
         for i, f in enumerate(step_fns):
             f()
             ev[s][i + 1].record()
-    end.record()
     torch.cuda.synchronize()
-    total = start.elapsed_time(end)
     stage = [sum(ev[s][i].elapsed_time(ev[s][i + 1]) for s in range(steps)) / steps for i in range(n)]
     return total, stage
+
+
+def time_alone(torch, fn, launches):
+    """ms per launch of `fn` run `launches` times back to back between one pair of events.
+    An event recorded between two kernels delays the second one's dispatch; for kernels of
+    tens of microseconds the per-stage figures of time_steps carry that delay, which the
+    profiler's kernel durations do not."""
+    fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(launches):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / launches
 
 
 def bench_cross(torch, W, dev, steps, warmup):
@@ -182,7 +206,8 @@ def bench_cross(torch, W, dev, steps, warmup):
         N.check("cross", lib.wan_flash_attn_qnorm(N.tensor4(q), N.tensor4(ck), N.tensor4(cv), N.tensor4(out),
                                                   B, H, Lq, L_TEXT, D, inv.data_ptr(), gq.data_ptr(),
                                                   None, None, D ** -0.5, lens_d.data_ptr(), s))
-    total, (t_prep, t_attn) = time_steps(torch, [prep, attn], steps, warmup)
+    total, (t_prep_step, t_attn_step) = time_steps(torch, [prep, attn], steps, warmup)
+    t_prep, t_attn = time_alone(torch, prep, steps), time_alone(torch, attn, steps)
     ssum = int(lens.sum())
     host = dict(q=q.cpu(), ck=ck.cpu(), cv=cv.cpu(), gq=gq.cpu(), lens=lens.tolist(),
                 flops=4.0 * H * Lq * D * ssum,
@@ -193,6 +218,9 @@ def bench_cross(torch, W, dev, steps, warmup):
         "workload": f"cross-attn B=2 Lq={Lq} Lkv={L_TEXT} H=24 d=128, seqlen_k={lens.tolist()}, "
                     "K/V from a [2, 512, 4096] N(0,1) context via text_embedding + lin_k/RMSNorm, lin_v",
         "ms_per_step": total / steps, "attn_kernel_ms": t_attn, "q_stats_ms": t_prep,
+        "attn_kernel_ms_in_step": t_attn_step, "q_stats_ms_in_step": t_prep_step,
+        "kernel_timing": "attn_kernel_ms / q_stats_ms: launches back to back between one event pair; "
+                         "*_in_step: an event pair around each launch within the interleaved steps",
         "tflops_kernel": flops / (t_attn * 1e-3) / 1e12,
         "hbm_gbs_kernel": byts / (t_attn * 1e-3) / 1e9,
         "frac_hbm_peak": byts / (t_attn * 1e-3) / 1e9 / PEAK_HBM_GBS,
@@ -444,6 +472,7 @@ def main():
     fs = FusedSelf(torch, W, t)
     total, (t_prep, t_attn) = time_steps(torch, [fs.prep, fs.attn], args.steps, args.warmup)
     ms = total / args.steps
+    t_attn_alone = time_alone(torch, fs.attn, min(args.steps, 20))
     flops = attn_flops(B, H, L, L)
     achieved = flops / (t_attn * 1e-3) / 1e12
     log(f"config C: step {ms:.3f} ms (prep {t_prep:.3f} ms, attention kernel {t_attn:.3f} ms) "
@@ -453,11 +482,15 @@ def main():
     if not args.no_extra:
         tA, hostA = make_inputs(torch, GRID_A, 1, dev)
         fA = FusedSelf(torch, W, tA)
-        totA, (pA, aA) = time_steps(torch, [fA.prep, fA.attn], args.steps, args.warmup)
+        totA, (pA_step, aA_step) = time_steps(torch, [fA.prep, fA.attn], args.steps, args.warmup)
+        pA, aA = time_alone(torch, fA.prep, args.steps), time_alone(torch, fA.attn, args.steps)
         LA = tA["q"].shape[1]
         extra["self_attn_L1080"] = {
             "workload": "fused self-attn B=2 L=1080 (grid 6x12x15) H=24 d=128",
             "ms_per_step": totA / args.steps, "attn_kernel_ms": aA, "prep_ms": pA,
+            "attn_kernel_ms_in_step": aA_step, "prep_ms_in_step": pA_step,
+            "kernel_timing": "attn_kernel_ms / prep_ms: launches back to back between one event pair; "
+                             "*_in_step: an event pair around each launch within the interleaved steps",
             "tflops_step": attn_flops(B, H, LA, LA) / (totA / args.steps * 1e-3) / 1e12,
             "tflops_kernel": attn_flops(B, H, LA, LA) / (aA * 1e-3) / 1e12}
         extra["cross_attn"], hostB = bench_cross(torch, W, dev, args.steps, args.warmup)
@@ -503,7 +536,8 @@ def main():
                      "bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic,
                      "traffic_source": traffic_note, "kernel_source_sha256": kernel_source_hash(),
-                     "kernel_ms": t_attn, "flops_per_launch": flops},
+                     "kernel_ms": t_attn, "flops_per_launch": flops,
+                     "kernel_ms_back_to_back": t_attn_alone},
         "cpu_baseline": cpu,
         "prep_ms": t_prep,
         "dit_s_per_step": extra.get("dit_E", {}).get("s_per_step"),
