@@ -64,6 +64,7 @@ constexpr int D = kHeadDim;             // 128
 constexpr int kTileElems = BN * D;      // one K or V tile: 64 rows of 256 B
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kSumBound = 65536.0f;   // per-lane tile sum of P that forces a rescale
+constexpr int kShortTableBytes = 16384; // persistent short-key kernel: gammas + key lengths
 
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
@@ -674,9 +675,12 @@ template __global__ void flash_fwd_kernel<4, kQNormRope>(const FlashArgs);
 // short sample are mostly start-up (query rows, first K/V tiles) and output store;
 // here, once an item's last S MFMAs are done, the next item's first two K tiles are
 // copied into the (then free) K buffers and its query rows loaded into the (then
-// free) Q registers, so that start-up overlaps the item's last tile and output store.
-// The output goes through LDS of its own (16 KB), so the K buffers can take the next
-// item's tiles meanwhile.  Each XCD owns a contiguous chunk of the items (a (batch,
+// free) Q registers, so that start-up overlaps the item's last tile; they are waited
+// for before the item's output stores, and nothing after the stores loads from global
+// memory before the next item is under way (the query gammas and key lengths sit in
+// LDS): a wait for a load issued after the stores would also wait for the stores.  The
+// output goes through the V buffer that does not hold the last V tile, so the K
+// buffers can take the next item's tiles meanwhile.  Each XCD owns a contiguous chunk of the items (a (batch,
 // head)'s K/V stay in one L2), its W workgroups striding through the chunk; the
 // batch index varies fastest over the items and W is odd, so consecutive items of a
 // workgroup alternate between the samples and long and short ones spread evenly.
@@ -686,13 +690,13 @@ struct ShortItem {
   int b, h, mblk, len, ntiles;
 };
 
-__device__ __forceinline__ ShortItem short_item(const FlashArgs& a, int it, int num_m) {
+__device__ __forceinline__ ShortItem short_item(const FlashArgs& a, int it, int num_m, const int* lens) {
   ShortItem r;
   r.b = it % a.B;
   const int rest = it / a.B;
   r.mblk = rest % num_m;
   r.h = rest / num_m;
-  r.len = a.seqlen_k != nullptr ? min(max(a.seqlen_k[r.b], 0), a.Lk) : a.seqlen_all;
+  r.len = lens[r.b];
   r.ntiles = (r.len + BN - 1) / BN;
   return r;
 }
@@ -715,11 +719,11 @@ __device__ __forceinline__ void load_q_raw(const FlashArgs& a, int b, int h, int
 
 // q' = bf16(bf16(q * inv_rms) * gamma), the reference's rounding points
 // (models/fast_dit.py:145-146, 156-160).
-__device__ __forceinline__ void norm_q(const FlashArgs& a, int h, int hh, float inv, bf16x8 qf[8]) {
+__device__ __forceinline__ void norm_q(const bf16* gamma, int h, int hh, float inv, bf16x8 qf[8]) {
 #pragma clang fp contract(off)
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) {
-    const bf16x8 g = *reinterpret_cast<const bf16x8*>(a.gamma_q + h * D + 16 * ks + 8 * hh);
+    const bf16x8 g = *reinterpret_cast<const bf16x8*>(gamma + h * D + 16 * ks + 8 * hh);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const bf16 t = (bf16)((float)qf[ks][j] * inv);
@@ -739,18 +743,41 @@ __device__ __forceinline__ const FlashArgs& kernel_args() {
   return *reinterpret_cast<const FlashArgs*>((const char*)p);
 }
 
+// s_waitcnt vmcnt(0) through the compiler's own builtin, so that its wait bookkeeping
+// knows every earlier vector memory access has completed (expcnt and lgkmcnt fields
+// at their maximum: no wait on those).
+__device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 template <int QP>
 __global__ __launch_bounds__(256, 2) void flash_short_kernel(const FlashArgs a0, int num_items) {
   constexpr int NW = 4, BM = NW * 32;
   __shared__ __attribute__((aligned(1024))) bf16 k_lds[2][kTileElems];
   __shared__ __attribute__((aligned(1024))) bf16 v_lds[2][kTileElems];
-  __shared__ __attribute__((aligned(1024))) bf16 o_lds[NW * 2048];
+  // the query gammas (H * 128) and then the per-sample key lengths (B), copied once
+  __shared__ __attribute__((aligned(16))) bf16 tab_lds[kShortTableBytes / 2];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n32 = lane & 31, hh = lane >> 5;
   const int num_m = (a0.Lq + BM - 1) / BM;
+  const int gamma_elems = QP != kQPlain ? a0.H * D : 0;
+  int* const lens = reinterpret_cast<int*>(tab_lds + gamma_elems);
+
+  // Each XCD (workgroup id % 8) owns one contiguous chunk of the items, so the
+  // K/V of a (batch, head) are fetched into one XCD's L2; the W workgroups of an
+  // XCD stride through its chunk.
+  const int xcd = blockIdx.x % kNumXcd, per = gridDim.x / kNumXcd;
+  const int base_n = num_items / kNumXcd, extra = num_items % kNumXcd;
+  const int chunk_end = (xcd + 1) * base_n + min(xcd + 1, extra);
+  int it = xcd * base_n + min(xcd, extra) + (int)(blockIdx.x / kNumXcd);
+  if (it >= chunk_end) return;
+
+  for (int i = tid; i < gamma_elems / 8; i += NW * 64)
+    *reinterpret_cast<bf16x8*>(tab_lds + 8 * i) = *reinterpret_cast<const bf16x8*>(a0.gamma_q + 8 * i);
+  for (int i = tid; i < a0.B; i += NW * 64)
+    lens[i] = a0.seqlen_k != nullptr ? min(max(a0.seqlen_k[i], 0), a0.Lk) : a0.seqlen_all;
+  __syncthreads();
 
   TileCore c;
   c.set_offsets(lane, a0.scale);
@@ -767,30 +794,28 @@ __global__ __launch_bounds__(256, 2) void flash_short_kernel(const FlashArgs a0,
     }
   };
 
-  // Each XCD (workgroup id % 8) owns one contiguous chunk of the items, so the
-  // K/V of a (batch, head) are fetched into one XCD's L2; the W workgroups of an
-  // XCD stride through its chunk.
-  const int xcd = blockIdx.x % kNumXcd, per = gridDim.x / kNumXcd;
-  const int base_n = num_items / kNumXcd, extra = num_items % kNumXcd;
-  const int chunk_end = (xcd + 1) * base_n + min(xcd + 1, extra);
-  int it = xcd * base_n + min(xcd, extra) + (int)(blockIdx.x / kNumXcd);
-  if (it >= chunk_end) return;
-  ShortItem cur = short_item(a0, it, num_m);
+  ShortItem cur = short_item(a0, it, num_m, lens);
   float inv = 1.f;
   prefetch_k(a0, cur);
   load_q_raw<QP>(a0, cur.b, cur.h, cur.mblk * BM + wave * 32 + n32, hh, c.qf, inv);
+  wait_vm_all();
+  // The V buffer not holding the last V tile of the latest item with tiles: free
+  // from that item's last barrier on, it stages the output.
+  int vfree = 1;
   for (;;) {
     c.reset();
-    if constexpr (QP != kQPlain) norm_q(kernel_args(), cur.h, hh, inv, c.qf);
+    if constexpr (QP != kQPlain) norm_q(tab_lds, cur.h, hh, inv, c.qf);
     const int nit = it + per;
+    ShortItem nxt{};
+    if (nit < chunk_end) nxt = short_item(kernel_args(), nit, num_m, lens);
     if (cur.ntiles > 0) {
       {
         const FlashArgs& a = kernel_args();
         vl.base = reinterpret_cast<const char*>(a.v.ptr + cur.b * a.v.sb + cur.h * a.v.sh);
       }
-      // this item's K0 / K1 (and query rows) have landed, for every wave; every
-      // wave is done with the previous item's V tiles
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      // this item's K0 / K1 (and query rows) have landed, for every wave (each waited
+      // for its own before its previous output store); every wave is done with the
+      // previous item's tiles and output staging
       __syncthreads();
       vl.issue(0, cur.len, v_lds[0], wave, lane);
       f32x16 sa0, sa1, sb0, sb1;
@@ -810,7 +835,7 @@ __global__ __launch_bounds__(256, 2) void flash_short_kernel(const FlashArgs a0,
         __syncthreads();
       };
       int t = 0;
-      const bf16* v_last = v_lds[0];
+      int vlast = 0;
       for (; t + 2 < cur.ntiles; t += 2) {
         step(t, k_lds[0], v_lds[1], k_lds[1], v_lds[0], sa0, sa1, sb0, sb1);
         step(t + 1, k_lds[1], v_lds[0], k_lds[0], v_lds[1], sb0, sb1, sa0, sa1);
@@ -819,34 +844,33 @@ __global__ __launch_bounds__(256, 2) void flash_short_kernel(const FlashArgs a0,
         step(t, k_lds[0], v_lds[1], k_lds[1], v_lds[0], sa0, sa1, sb0, sb1);
         sa0 = sb0;
         sa1 = sb1;
-        v_last = v_lds[1];
+        vlast = 1;
         ++t;
       }
       // Every wave has passed the barrier after the last S MFMAs: the K buffers
       // are free for the next item's first tiles.
       if (nit < chunk_end) {
         const FlashArgs& a = kernel_args();
-        const ShortItem ni = short_item(a, nit, num_m);
-        prefetch_k(a, ni);
-        load_q_raw<QP>(a, ni.b, ni.h, ni.mblk * BM + wave * 32 + n32, hh, c.qf, inv);
+        prefetch_k(a, nxt);
+        load_q_raw<QP>(a, nxt.b, nxt.h, nxt.mblk * BM + wave * 32 + n32, hh, c.qf, inv);
       }
       if (cur.ntiles * BN > cur.len) c.mask_tile(sa0, sa1, t * BN, cur.len);
       bf16x8 pb[4];
       c.finish(sa0, sa1, c.exp_tile(sa0, sa1, pb), pb);
-      c.pv(pb, v_last);
+      c.pv(pb, v_lds[vlast]);
+      vfree = vlast ^ 1;
     } else if (nit < chunk_end) {
       const FlashArgs& a = kernel_args();
-      prefetch_k(a, short_item(a, nit, num_m));
+      prefetch_k(a, nxt);
+      load_q_raw<QP>(a, nxt.b, nxt.h, nxt.mblk * BM + wave * 32 + n32, hh, c.qf, inv);
     }
-    // The next item's query rows go into the Q registers (free now) before this
-    // item's output is normalised and stored, so their loads overlap the store.
+    // The next item's tiles and query rows were issued before this item's last tile:
+    // they are waited for here, before the output stores, so that nothing after the
+    // stores waits for a load issued before them (a wait for such a load would also
+    // wait for the stores, which complete out of order with loads).
+    wait_vm_all();
     const FlashArgs& a = kernel_args();
-    ShortItem nxt{};
-    if (nit < chunk_end) {
-      nxt = short_item(a, nit, num_m);
-      if (cur.ntiles == 0) load_q_raw<QP>(a, nxt.b, nxt.h, nxt.mblk * BM + wave * 32 + n32, hh, c.qf, inv);
-    }
-    c.store_out(o_lds + wave * 2048, a.o + cur.b * a.o_sb + cur.h * a.o_sh, a.o_st,
+    c.store_out(v_lds[vfree] + wave * 2048, a.o + cur.b * a.o_sb + cur.h * a.o_sh, a.o_st,
                 cur.mblk * BM + wave * 32, a.Lq, lane);
     if (nit >= chunk_end) break;
     it = nit;
@@ -912,7 +936,9 @@ template <int QP>
 int launch_qp(const FlashArgs& a, hipStream_t s) {
   if (a.Lk <= kShortKeys) {
     if constexpr (QP != kQNormRope) {
-      if (a.seqlen_k != nullptr) return launch_short<QP>(a, s);
+      // (the persistent kernel keeps the query gammas and the key lengths in LDS)
+      const int table = (QP != kQPlain ? a.H * D * 2 : 0) + a.B * 4;
+      if (a.seqlen_k != nullptr && table <= kShortTableBytes) return launch_short<QP>(a, s);
     }
     return launch_nw<4, QP>(a, s);
   }
