@@ -364,6 +364,32 @@ def test_cross_config_b_text_recipe(W, lens):
     assert torch.isfinite(out.float()).all() and e <= 5e-3
 
 
+@pytest.mark.parametrize("fused,B,H", [(True, 3, 64), (False, 3, 64), (True, 9, 8), (False, 9, 8)])
+def test_cross_lengths_table_limits(W, fused, B, H):
+    """The persistent short-key kernel keeps the query gammas (H x 128) and the key lengths
+    (B) in a 16 KB LDS table: at 64 heads with the fused Q norm they do not fit and the
+    plain kernel runs instead; without the norm (no gammas) or at 8 heads they fit.  Both
+    against the oracle, with lengths 0, 1, a partial tile and the full 512."""
+    Lq, Lk = 300, 512
+    lens = ([0, 1, 512, 130, 64, 511, 2, 200, 17] * 2)[:B]
+    q, ck, cv = _bf((B, Lq, H, D), 501 + H), _bf((B, Lk, H, D), 502 + H), _bf((B, Lk, H, D), 503 + H)
+    gq = _gammas(H * D, 504, True)
+    sk = torch.tensor(lens, dtype=torch.int32).to(DEV)
+    if fused:
+        out = W.ops.cross_attn_fused(*_d(q, ck, cv, gq), 1e-6, sk, SCALE).cpu()
+        qn = ref.rms(q.reshape(B, Lq, H * D), gq).view(B, Lq, H, D)
+    else:
+        out = W.ops.cross_attn(*_d(q, ck, cv), sk, SCALE).cpu()
+        qn = q
+    want = ref.sdpa(qn.float(), ck.float(), cv.float(), seqlen_k=lens)
+    keep = [b for b in range(B) if lens[b] > 0]
+    for b in range(B):
+        if lens[b] == 0:
+            assert torch.count_nonzero(out[b]) == 0
+    assert torch.isfinite(out.float()).all()
+    assert ref.rel_rms(out[keep], want[keep]) <= 5e-3
+
+
 @pytest.mark.parametrize("fused", [False, True])
 def test_persistent_cross_mixed_lengths(W, fused):
     """Per-sample key lengths select the persistent short-key kernel: each workgroup walks
