@@ -192,3 +192,37 @@ def test_noalloc_rejects_rows_beyond_its_scratch(W):
     assert rc == 2 and "static scratch" in N.last_error()
     rc = lib.wan_cross_attn_fused_noalloc(t, t, t, t, 1, 24, 16, 16, 128, 256, 1e-6, 0.0, None, None)
     assert rc == 2 and "softmax_scale" in N.last_error()
+
+
+def test_qkv_gemm_and_sumsq_prep_validation_without_launching(W):
+    """wan_qkv_proj_sumsq and wan_rms_norm_qk_sumsq refuse unsupported shapes, strides and
+    missing operands before any device call."""
+    N = W._native
+    lib = N.lib()
+    P = 256   # a 16-byte aligned stand-in address: nothing is launched
+    gemm = lib.wan_qkv_proj_sumsq
+    # N not a multiple of 256, K not a multiple of 64
+    assert gemm(P, P, P, P, P, 64, 384, 128, 128, 128, 384, 128, None) == 2 and "multiple of 256" in N.last_error()
+    assert gemm(P, P, P, P, P, 64, 512, 96, 96, 96, 512, 128, None) == 2 and "multiple" in N.last_error()
+    # sq_cols beyond N or not a multiple of 64
+    assert gemm(P, P, P, P, P, 64, 512, 128, 128, 128, 512, 576, None) == 1 and "sq_cols" in N.last_error()
+    assert gemm(P, P, P, P, P, 64, 512, 128, 128, 128, 512, 96, None) == 1 and "sq_cols" in N.last_error()
+    # row strides shorter than the rows, or not multiples of 8 elements
+    assert gemm(P, P, P, P, P, 64, 512, 128, 64, 128, 512, 128, None) == 1 and "strides" in N.last_error()
+    assert gemm(P, P, P, P, P, 64, 512, 128, 132, 128, 512, 128, None) == 1 and "strides" in N.last_error()
+    # strides beyond the 32-bit tile offsets
+    assert gemm(P, P, P, P, P, 64, 512, 128, 1 << 23, 128, 512, 128, None) == 2
+    # a missing bias, misaligned output
+    assert gemm(P, P, None, P, P, 64, 512, 128, 128, 128, 512, 128, None) == 1 and "aligned" in N.last_error()
+    assert gemm(P, P, P, P + 2, P, 64, 512, 128, 128, 128, 512, 128, None) == 1
+    # K = 0 is refused (no tile to accumulate); M = 0 is nothing to do
+    assert gemm(P, P, P, P, P, 64, 512, 0, 128, 128, 512, 128, None) == 1 and "bad sizes" in N.last_error()
+    assert gemm(P, P, P, P, P, 0, 512, 128, 128, 128, 512, 128, None) == 0
+
+    t = N.WanTensor(64, 24 * 128 * 16, 24 * 128, 128)
+    prep = lib.wan_rms_norm_qk_sumsq
+    assert prep(t, P, 1, 16, 24, 128, P, 1e-6, P, P, None, P, None) == 1 and "required" in N.last_error()
+    assert prep(t, P, 1, 16, 24, 128, P, 1e-6, P, P, P + 4, P, None) == 1 and "aligned" in N.last_error()
+    assert prep(t, P, 1, 16, 40, 128, P, 1e-6, P, P, P, P, None) == 2 and "partial sums" in N.last_error()
+    assert prep(t, P, 1, 16, 24, 64, P, 1e-6, P, P, P, P, None) == 2 and "head_dim" in N.last_error()
+    assert prep(t, P, 0, 16, 24, 128, P, 1e-6, P, P, P, P, None) == 0
