@@ -23,7 +23,7 @@ attention, on seeded N(0,1) projections already resident in HBM.
 
 Prints one JSON line on stdout.  Usage:
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--cpu-seconds S] [--no-cpu-baseline]
-  python bench.py --profile-config {A,B,C,QKV} [--steps K]   (one config's steps only, for rocprofv3)
+  python bench.py --profile-config {A,B,C,QKV,QKVGEMM} [--steps K]   (one config's steps only, for rocprofv3)
 """
 import argparse
 import json
@@ -277,6 +277,31 @@ def bench_qkv(torch, W, dev, steps, warmup):
         "hipblaslt_tflops": flops / (t_blas * 1e-3) / 1e12, "sumsq_gemm_tflops": flops / (t_gemm * 1e-3) / 1e12}}
 
 
+def qkv_gemms_alone(torch, W, dev, launches):
+    """The QKV projection GEMM with the sums of squares and hipBLASLt's F.linear on the same
+    inputs, each `launches` times back to back with nothing in between (for counters that
+    other kernels between the launches would disturb, such as the L2 misses)."""
+    import torch.nn.functional as F
+    N_, lib = W._native, W._native.lib()
+    L = GRID_C[0] * GRID_C[1] * GRID_C[2]
+    C = H * D
+    g = torch.Generator(device=dev).manual_seed(21)
+    x = torch.randn(B * L, C, device=dev, generator=g).to(torch.bfloat16)
+    w = (torch.randn(3 * C, C, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    bias = (torch.randn(3 * C, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    out = torch.empty(B * L, 3 * C, device=dev, dtype=torch.bfloat16)
+    ss = torch.empty(4 * H, B * L, device=dev, dtype=torch.float32)
+    s = torch.cuda.current_stream().cuda_stream
+
+    def gemm():
+        N_.check("qkv gemm", lib.wan_qkv_proj_sumsq(x.data_ptr(), w.data_ptr(), bias.data_ptr(), out.data_ptr(),
+                                                    ss.data_ptr(), B * L, 3 * C, C, C, C, 3 * C, 2 * C, s))
+    res = {}
+    for name, fn in (("sumsq_gemm_ms", gemm), ("hipblaslt_gemm_ms", lambda: F.linear(x, w, bias))):
+        res[name] = time_alone(torch, fn, launches)
+    return res
+
+
 def bench_torch_sdpa(torch, t, steps, warmup):
     """torch's own F.scaled_dot_product_attention (flash backend) on the config C shapes:
     plain attention of the same q/k/v sizes (no norm, no rotation), for comparison."""
@@ -423,7 +448,7 @@ def main():
     ap.add_argument("--no-dit", action="store_true", help="skip the block (D) and 30-layer DiT (E) runs")
     ap.add_argument("--dit-steps", type=int, default=10)
     ap.add_argument("--dit-layers", type=int, default=30)
-    ap.add_argument("--profile-config", choices=["A", "B", "C", "QKV"], default=None,
+    ap.add_argument("--profile-config", choices=["A", "B", "C", "QKV", "QKVGEMM"], default=None,
                     help="only run the timed steps of one attention config, or of the two QKV "
                          "projection routes (for rocprofv3 counters)")
     ap.add_argument("--profile-copy", type=int, default=0, metavar="BYTES",
@@ -455,6 +480,8 @@ def main():
         if args.profile_config == "B":
             r, _ = bench_cross(torch, W, dev, args.steps, args.warmup)
             log(f"config B: attention kernel {r['attn_kernel_ms']:.4f} ms")
+        elif args.profile_config == "QKVGEMM":
+            log(f"QKV GEMMs alone: {json.dumps(qkv_gemms_alone(torch, W, dev, args.steps))}")
         elif args.profile_config == "QKV":
             r = bench_qkv(torch, W, dev, args.steps, args.warmup)["qkv_projection"]
             log(f"QKV projection: gemm {r['sumsq_gemm_ms']:.4f} ms, hipBLASLt {r['hipblaslt_gemm_ms']:.4f} ms")
