@@ -342,6 +342,19 @@ struct TileCore {
     l_run += rs;
   }
 
+  // The reference point from the exact row max of the first tile's scores.  Left at -inf,
+  // the first tile's exponentials overflow in qk_exp and finish() computes them again
+  // (for an item of two tiles, half of all its exponentials).  Keys past the length in
+  // a partial first tile are copies of the last valid key, so they do not raise the max.
+  __device__ __forceinline__ void init_max(const f32x16& s0, const f32x16& s1) {
+    float mx = fmaxf(s0[0], s0[1]);
+#pragma unroll
+    for (int r = 2; r < 16; ++r) mx = fmaxf(mx, s0[r]);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s1[r]);
+    m_run = pair_max(mx) * sl2;
+  }
+
   // Sets the scores of keys >= len to -inf (a partial last tile starting at key kt).
   __device__ __forceinline__ void mask_tile(f32x16& s0, f32x16& s1, int kt, int len) const {
 #pragma unroll
@@ -579,6 +592,7 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
       // ring of four); the tiles issued after it land while S(0) is computed,
       // and this barrier publishes them and frees K0
       c.qk(k_lds[0], sa0, sa1);
+      c.init_max(sa0, sa1);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
     } else {
@@ -586,6 +600,7 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
       c.qk(k_lds[0], sa0, sa1);
+      c.init_max(sa0, sa1);
       __syncthreads();  // every wave is done with K0 before it is overwritten
     }
 
@@ -821,6 +836,7 @@ __global__ __launch_bounds__(256, 2) void flash_short_kernel(const FlashArgs a0,
       f32x16 sa0, sa1, sb0, sb1;
       // V0 lands while S(0) is computed; the barrier publishes it and frees K0
       c.qk(k_lds[0], sa0, sa1);
+      c.init_max(sa0, sa1);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
 
