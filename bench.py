@@ -15,7 +15,7 @@ attention, on seeded N(0,1) projections already resident in HBM.
               torch SDPA) on the host cores over the whole config C workload in fp32,
               median of up to 3 runs; configs A and B and bf16 under "table"
   extra       the same path at L=1080 and the masked cross-attention (Lq=7854,
-              512 text keys, per-sample lengths U[16, 512]), with HBM GB/s; torch's
+              512 text keys, per-sample lengths [470, 123]), with HBM GB/s; torch's
               own flash SDPA on the config C shapes, for comparison; the q/k/v
               projection + QK-RMSNorm prep by hipBLASLt and by the sums-of-squares GEMM; one
               WanAttentionBlock (D) and the 30-layer DiT, 10 UniPC steps (E):
@@ -441,7 +441,9 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    # after idle the part raises its clocks over the first ~0.1 s of work: 100 untimed steps
+    # (~0.15 s at config C) put the timed steps at the steady state
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--cpu-seconds", type=float, default=25.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
