@@ -1,8 +1,8 @@
 """CPU oracle of the Wan DiT attention path — TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
-this module, and only as the checker (or, for the CPU baseline, as the thing
-timed on host cores).  The product path (wan2-ti2v-5b_amd) never calls it.
+this module, and only to check results against (or, for the CPU baseline, as the
+thing timed on host cores).  The product path (wan2-ti2v-5b_amd) never calls it.
 
 It restates, in plain torch-on-CPU (and numpy for the brute-force forms), the
 reference's arithmetic for this path, with the reference's bf16 rounding points
@@ -25,7 +25,7 @@ when given bf16 tensors and without them when given fp32 tensors:
   unpatchify         wan/modules/model.py:496-519
   adaln              models/fast_dit.py:172-181,280,294,306-311 with WanLayerNorm
                      (wan/modules/model.py:89-99): one bf16 adaLN stage of a block
-  layer_norm64       float64 numpy LayerNorm (biased variance), the checker of adaln
+  layer_norm64       float64 numpy LayerNorm (biased variance), what adaln is checked against
 
 Each function is pinned by tests/test_oracle.py (closed forms, invariants,
 library routines and float64 brute force); see that file's header.
