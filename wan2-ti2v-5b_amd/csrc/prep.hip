@@ -35,7 +35,9 @@ __device__ __forceinline__ void rope8(float u[8], const float* cos_row,
 
 // One wave per token row: sum of squares over all H*128 channels, then
 // optionally the normalised (and rotated) row.  NCH: 8-channel chunks per lane
-// (H*16 <= 64*NCH), so the row's loads are issued unconditionally together.
+// (H*16 <= 64*NCH), so the row's loads are issued unconditionally together.  The
+// rows are read once here: non-temporal loads (4% faster at B=2, L=7854 than plain
+// ones; the written rows stay cacheable, the attention kernel reads them next).
 template <int NCH>
 __device__ __forceinline__ void rms_prep_rows(const PrepArgs& a, int block) {
   const int lane = threadIdx.x & 63;
@@ -55,7 +57,7 @@ __device__ __forceinline__ void rms_prep_rows(const PrepArgs& a, int block) {
 #pragma unroll
       for (int i = 0; i < NCH; ++i) {
         const int c = lane + 64 * i;
-        if (c < nchunks) xv[i] = *reinterpret_cast<const bf16x8*>(row + (c >> 4) * a.x.sh + (c & 15) * 8);
+        if (c < nchunks) xv[i] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(row + (c >> 4) * a.x.sh + (c & 15) * 8));
       }
     }
   } else {
@@ -64,7 +66,7 @@ __device__ __forceinline__ void rms_prep_rows(const PrepArgs& a, int block) {
       const int c = lane + 64 * i;
       if (c < nchunks) {
         const int h = c >> 4, d0 = (c & 15) * 8;
-        xv[i] = *reinterpret_cast<const bf16x8*>(row + h * a.x.sh + d0);
+        xv[i] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(row + h * a.x.sh + d0));
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const float f = (float)xv[i][j];
