@@ -36,8 +36,9 @@ __device__ __forceinline__ void rope8(float u[8], const float* cos_row,
 // One wave per token row: sum of squares over all H*128 channels, then
 // optionally the normalised (and rotated) row.  NCH: 8-channel chunks per lane
 // (H*16 <= 64*NCH), so the row's loads are issued unconditionally together.  The
-// rows are read once here: non-temporal loads (4% faster at B=2, L=7854 than plain
-// ones; the written rows stay cacheable, the attention kernel reads them next).
+// rows are read once here: non-temporal loads (4% faster alone at B=2, L=7854 than
+// plain ones, ~2 us a launch, below what a whole block forward resolves; the written
+// rows stay cacheable, the attention kernel reads them next).
 template <int NCH>
 __device__ __forceinline__ void rms_prep_rows(const PrepArgs& a, int block) {
   const int lane = threadIdx.x & 63;
