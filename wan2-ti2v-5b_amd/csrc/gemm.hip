@@ -23,11 +23,12 @@
 // M-tiles per N-tile, each XCD owning a contiguous range, so the tiles running together
 // on an XCD share x and w rows in its L2.
 //
-// At the QKV shape (M 15708, N 9216, K 3072) it reaches 1.20-1.27 PFLOP/s, 84-86% of
+// At the QKV shape (M 15708, N 9216, K 3072) it reaches 1.28-1.31 PFLOP/s, 86-88% of
 // hipBLASLt's F.linear timed beside it, with output bit-identical.  Both are power
 // limited (all-zero operands run either ~25% faster); on zeros this kernel's k-loop is
-// ~13% slower per tile than hipBLASLt's, and 4 waves of 128 x 128 (a third less LDS
-// read traffic, one wave per SIMD) measured slower than this tiling.
+// ~13% slower per tile than hipBLASLt's.  4 waves of 128 x 128 (a third less LDS read
+// traffic, one wave per SIMD) run the loop at a higher clock (1.72 vs 1.58 GHz) but in
+// more cycles per tile, and tie with this tiling at best.
 #include "common.h"
 
 #include <type_traits>
@@ -141,6 +142,16 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_rowsq_kernel(const GemmA
   for (int b = 0; b < C::TN; ++b) wrow[b] = (wn * C::TN + b) * 32 + l32;
   const int sw = C::swz(l32);
 
+  // the bias of this wave's columns, loaded before the k-loop: in the epilogue its
+  // loads stood first on the critical path (1-1.3% of the launch)
+  constexpr int kCols = C::TN * 32;              // this wave's columns (64 or 128)
+  bf16x4 bias_r[C::TN][4];
+#pragma unroll
+  for (int nb = 0; nb < C::TN; ++nb)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      bias_r[nb][g] = *reinterpret_cast<const bf16x4*>(a.bias + n0 + wn * kCols + nb * 32 + 8 * g + 4 * hh);
+
   f32x16 acc[C::TN][C::TM];
 #pragma unroll
   for (int i = 0; i < C::TN; ++i)
@@ -220,7 +231,6 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_rowsq_kernel(const GemmA
   // each 64 of this wave's columns, then the block staged through this wave's LDS
   // (row-major, chunk c of row r at position c ^ (r % chunks)) and stored as whole row
   // segments.
-  constexpr int kCols = C::TN * 32;              // this wave's columns (64 or 128)
   constexpr int kChunks = kCols / 8;
   bf16* stage = &xs[0][0] + wave * 32 * kCols;
   const int ncol0 = n0 + wn * kCols;
@@ -232,7 +242,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_rowsq_kernel(const GemmA
     for (int nb = 0; nb < C::TN; ++nb) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const bf16x4 b4 = *reinterpret_cast<const bf16x4*>(a.bias + ncol0 + nb * 32 + 8 * g + 4 * hh);
+        const bf16x4 b4 = bias_r[nb][g];
         bf16x4 v;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
