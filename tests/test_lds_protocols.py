@@ -109,6 +109,7 @@ def _ring4_ops(n, *, drop_epilogue_barrier=False, v_ring_of_two=False, no_wait_o
     ops += [("read", K(0), ("K", 0)), ("wait",), ("bar",)]
 
     def step(t):
+        ops.append(("read", K(t + 1), ("K", t + 1)))     # S(t+1) and the softmax of tile t
         if t % 2 == 0:
             for tile in (t + 3, t + 4):
                 if tile < n:
@@ -116,8 +117,7 @@ def _ring4_ops(n, *, drop_epilogue_barrier=False, v_ring_of_two=False, no_wait_o
             for tile in (t + 2, t + 3):
                 if tile < n:
                     ops.append(("issue", V(tile), ("V", tile)))
-        ops.append(("read", K(t + 1), ("K", t + 1)))
-        ops.append(("read", V(t), ("V", t)))
+        ops.append(("read", V(t), ("V", t)))             # PV of tile t
         if t % 2 == 1:
             ops.extend(([] if no_wait_on_odd else [("wait",)]) + [("bar",)])
 

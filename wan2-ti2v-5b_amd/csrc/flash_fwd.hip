@@ -628,14 +628,16 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_fwd_kernel(const FlashArgs a
       // waits for them and publishes them with the barrier.
       auto step4 = [&](int t, int odd, const bf16* k_next, const bf16* v_cur, bf16* kf3, bf16* kf4,
                        bf16* vf2, bf16* vf3, f32x16& c0, f32x16& c1, f32x16& n0, f32x16& n1) {
+        bf16x8 pb[4];
+        c.finish(c0, c1, c.qk_exp(k_next, n0, n1, c0, c1, pb), pb);
+        // the copies go out between the softmax and PV: issued at the step's start, their
+        // burst held up both waves of each SIMD at once (2.3-2.7% slower at L=7854)
         if (!odd) {
           if (t + 3 < ntiles) kl.issue(t + 3, len, kf3, wave, lane);
           if (t + 4 < ntiles) kl.issue(t + 4, len, kf4, wave, lane);
           if (t + 2 < ntiles) vl.issue(t + 2, len, vf2, wave, lane);
           if (t + 3 < ntiles) vl.issue(t + 3, len, vf3, wave, lane);
         }
-        bf16x8 pb[4];
-        c.finish(c0, c1, c.qk_exp(k_next, n0, n1, c0, c1, pb), pb);
         c.pv(pb, v_cur);
         if (odd) {
           asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
