@@ -53,7 +53,11 @@ __device__ __forceinline__ uint32_t lds_addr(const bf16* p) {
 
 // 16-byte global -> LDS copy (lane l writes LDS bytes m0 + 16 l ..), from inline asm so
 // the compiler's LDS wait counting does not see it (see flash_fwd.hip); completion is
-// waited for explicitly before the barrier that publishes a stage.
+// waited for explicitly before the barrier that publishes a stage.  A memory instruction
+// needs 5 wait states after a VALU write (v_readfirstlane / v_readlane) of an SGPR it
+// reads, and the compiler does not pad that for inline asm: the scalar base of this copy
+// and of flash_fwd.hip's must come from scalar code (tests/test_isa_hazards.py checks
+// the compiled kernels).
 __device__ __forceinline__ void dma16(const char* sbase, uint32_t voff, uint32_t lds) {
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                :: "v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
