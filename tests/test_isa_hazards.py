@@ -110,7 +110,28 @@ _Zk:
     assert not valu_sgpr_hazards(rewritten)
 
 
-@pytest.mark.parametrize("src", ["flash_fwd.hip", "gemm.hip"])
+def _sources_with_inline_memory_asm():
+    """Every source file whose inline assembly names a vector memory instruction."""
+    out = []
+    for name in sorted(os.listdir(CSRC)):
+        if name.endswith((".hip", ".h")):
+            with open(os.path.join(CSRC, name)) as f:
+                text = f.read()
+            if re.search(r'asm\s*(volatile\s*)?\(\s*"[^"]*(global|buffer|scratch|flat)_(load|store|atomic)', text):
+                out.append(name)
+    return out
+
+
+SCANNED = ["flash_fwd.hip", "gemm.hip"]
+
+
+def test_every_inline_memory_asm_source_is_scanned():
+    # equality: a new source with such assembly must join the scan, and the search
+    # must still find the two that have it
+    assert _sources_with_inline_memory_asm() == SCANNED
+
+
+@pytest.mark.parametrize("src", SCANNED)
 def test_no_valu_sgpr_write_before_a_memory_read(src, tmp_path):
     build = _build_module()
     if not os.path.exists(build.HIPCC) and shutil.which("hipcc") is None:
