@@ -23,7 +23,7 @@ attention, on seeded N(0,1) projections already resident in HBM.
 
 Prints one JSON line on stdout.  Usage:
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--cpu-seconds S] [--no-cpu-baseline]
-  python bench.py --profile-config {A,B,C,QKV,QKVGEMM} [--steps K]   (one config's steps only, for rocprofv3)
+  python bench.py --profile-config {A,B,C,D,QKV,QKVGEMM} [--steps K]   (one config's steps only, for rocprofv3)
 """
 import argparse
 import json
@@ -319,9 +319,9 @@ def bench_torch_sdpa(torch, t, steps, warmup):
         "ms": ms, "tflops": attn_flops(B, H, L, L) / (ms * 1e-3) / 1e12}}
 
 
-def bench_dit(torch, W, dev, steps, layers):
-    """Config D (one WanAttentionBlock at L=7854) and config E (the 30-layer DiT, 10 UniPC
-    steps at 704x544x81) with random bf16 weights (std 0.02) and the HIP attention path."""
+def dit_setup(torch, W, dev, layers):
+    """A `layers`-layer DiT at 704x544x81 with random bf16 weights (std 0.02), the HIP
+    attention path, both prompts' cross K/V set and one warm-up forward done."""
     cfg = W.model.WanConfig()
     model = W.model.random_model(cfg, num_layers=layers, device=dev, seed=0)
     fast = W.fast_dit.FastWanDiT(model, GRID_C, cfg.sample_guide_scale, attn_impl="hip", cross_impl="hip")
@@ -332,21 +332,49 @@ def bench_dit(torch, W, dev, steps, layers):
     ctx_n = torch.randn(1, cfg.text_len, cfg.text_dim, generator=g).to(dev)
     image_latent = torch.randn(cfg.in_dim, 1, 2 * h, 2 * w, generator=g).to(dev)
     fast.set_context(ctx_c, ctx_n)
-    out = fast(latent, torch.tensor(999))                    # warm-up (GEMM heuristics, allocator)
+    fast(latent, torch.tensor(999))                          # warm-up (GEMM heuristics, allocator)
     torch.cuda.synchronize()
+    return cfg, fast, latent, image_latent
+
+
+def block_inputs(torch, fast, latent):
+    """The first block and its inputs as the DiT gives them at t = 500."""
+    _, e0 = fast.time_rows(torch.tensor(500))
+    ck, cv = fast.context[0]
+    return fast.blocks[0], (fast.patch(latent), e0, fast.cos, fast.sin, ck, cv)
+
+
+def profile_block(torch, W, dev, steps):
+    """Only `steps` forwards of one WanAttentionBlock at L=7854 (for rocprofv3)."""
+    _, fast, latent, _ = dit_setup(torch, W, dev, 1)
+    blk, inputs = block_inputs(torch, fast, latent)
+    for _ in range(2):
+        blk(*inputs)
+    e_a, e_b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e_a.record()
+    for _ in range(steps):
+        blk(*inputs)
+    e_b.record()
+    torch.cuda.synchronize()
+    return e_a.elapsed_time(e_b) / steps
+
+
+def bench_dit(torch, W, dev, steps, layers):
+    """Config D (one WanAttentionBlock at L=7854) and config E (the 30-layer DiT, 10 UniPC
+    steps at 704x544x81) with random bf16 weights (std 0.02) and the HIP attention path."""
+    cfg, fast, latent, image_latent = dit_setup(torch, W, dev, layers)
 
     # config D: one block, its inputs as in the DiT
-    e, e0 = fast.time_rows(torch.tensor(500))
-    x = fast.patch(latent)
-    ck, cv = fast.context[0]
-    blk = fast.blocks[0]
+    blk, inputs = block_inputs(torch, fast, latent)
+    x = inputs[0]
     for _ in range(2):
-        blk(x, e0, fast.cos, fast.sin, ck, cv)
+        blk(*inputs)
     e_a, e_b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     e_a.record()
     for _ in range(5):
-        y = blk(x, e0, fast.cos, fast.sin, ck, cv)
+        y = blk(*inputs)
     e_b.record()
     torch.cuda.synchronize()
     block_ms = e_a.elapsed_time(e_b) / 5
@@ -450,9 +478,9 @@ def main():
     ap.add_argument("--no-dit", action="store_true", help="skip the block (D) and 30-layer DiT (E) runs")
     ap.add_argument("--dit-steps", type=int, default=10)
     ap.add_argument("--dit-layers", type=int, default=30)
-    ap.add_argument("--profile-config", choices=["A", "B", "C", "QKV", "QKVGEMM"], default=None,
-                    help="only run the timed steps of one attention config, or of the two QKV "
-                         "projection routes (for rocprofv3 counters)")
+    ap.add_argument("--profile-config", choices=["A", "B", "C", "D", "QKV", "QKVGEMM"], default=None,
+                    help="only run the timed steps of one attention config, of one block (D), or "
+                         "of the two QKV projection routes (for rocprofv3)")
     ap.add_argument("--profile-copy", type=int, default=0, metavar="BYTES",
                     help="only run 10 device-to-device copies of BYTES (HBM counter calibration)")
     args = ap.parse_args()
@@ -482,6 +510,8 @@ def main():
         if args.profile_config == "B":
             r, _ = bench_cross(torch, W, dev, args.steps, args.warmup)
             log(f"config B: attention kernel {r['attn_kernel_ms']:.4f} ms")
+        elif args.profile_config == "D":
+            log(f"config D: {profile_block(torch, W, dev, args.steps):.3f} ms per block")
         elif args.profile_config == "QKVGEMM":
             log(f"QKV GEMMs alone: {json.dumps(qkv_gemms_alone(torch, W, dev, args.steps))}")
         elif args.profile_config == "QKV":
