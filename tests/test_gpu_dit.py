@@ -58,6 +58,31 @@ def test_tiny_dit_hip_vs_oracle(W):
     assert e_hip < 3e-2 and e_hip < 1.5 * e_sdpa + 5e-3
 
 
+def test_denoise_never_makes_the_host_wait(W):
+    """The denoising loop (DiT forwards, UniPC steps on the device, the image-latent blend)
+    issues nothing that makes the host wait for the GPU: torch's sync debug mode raises on
+    any such operation.  The latent is the same as with the mode off."""
+    cfg = W.model.WanConfig(**TINY)
+    m = W.model.random_model(cfg, device=DEV, std=0.05, seed=0)
+    grid = (3, 4, 5)
+    g = torch.Generator().manual_seed(3)
+    latent = torch.randn(4, 3, 8, 10, generator=g).to(DEV)
+    image = torch.randn(4, 1, 8, 10, generator=g).to(DEV)
+    ctx_c, ctx_n = torch.randn(1, 7, 64, generator=g), torch.randn(1, 7, 64, generator=g)
+    fast = W.fast_dit.FastWanDiT(m, grid, 5.0, attn_impl="hip", cross_impl="hip", pointwise_impl="hip")
+    fast.set_context(ctx_c.to(DEV), ctx_n.to(DEV))
+    free = W.fast_dit.denoise(fast, latent, 4, 5.0, image_latent=image)
+    torch.cuda.synchronize()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        watched = W.fast_dit.denoise(fast, latent, 4, 5.0, image_latent=image)
+    finally:
+        torch.cuda.set_sync_debug_mode(0)
+    torch.cuda.synchronize()
+    assert torch.isfinite(watched.float()).all()
+    assert torch.equal(watched, free)
+
+
 def _full_block(W, seed=0):
     cfg = W.model.WanConfig()
     m = W.model.random_model(cfg, num_layers=1, device=DEV, seed=seed)

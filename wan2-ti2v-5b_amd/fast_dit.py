@@ -296,7 +296,13 @@ class FastWanDiT:
         blocks' modulation input [1, F, 6, C]."""
         m = self.model
         frame_t = float(t) * (torch.arange(self.num_frames) > 0).double()
-        sincos = sinusoidal_embedding_1d(m.freq_dim, frame_t).to(torch.bfloat16).to(self.device)
+        sincos = sinusoidal_embedding_1d(m.freq_dim, frame_t).to(torch.bfloat16)
+        if self.device.type == "cuda":
+            # through pinned memory without a wait: a copy from pageable memory would block
+            # the host until the stream drained, once per denoising step
+            sincos = sincos.pin_memory().to(self.device, non_blocking=True)
+        else:
+            sincos = sincos.to(self.device)
         emb = m.time_embedding(sincos.unsqueeze(0))
         return emb, m.time_projection(emb).view(1, self.num_frames, 6, m.dim)
 
