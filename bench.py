@@ -19,7 +19,8 @@ attention, on seeded N(0,1) projections already resident in HBM.
               own flash SDPA on the config C shapes, for comparison; the q/k/v
               projection + QK-RMSNorm prep by hipBLASLt and by the sums-of-squares GEMM; one
               WanAttentionBlock (D) and the 30-layer DiT, 10 UniPC steps (E):
-              dit_s_per_step is the second half of the metric
+              dit_s_per_step is the second half of the metric; the same DiT at the
+              368x480x21 size (1080 tokens) as dit_E_L1080
 
 Prints one JSON line on stdout.  Usage:
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--cpu-seconds S] [--no-cpu-baseline]
@@ -127,6 +128,30 @@ class FusedSelf:
             t["cos"].data_ptr(), t["sin"].data_ptr(), D ** -0.5, None, self.stream))
 
 
+SETTLE_SECONDS = 0.3
+
+
+def settle(torch, step_fns, seconds=None):
+    """Untimed repetitions of the step for about `seconds` of device time before the warm-up
+    steps.  After idle the part raises its clocks over the first ~0.1 s of work, so a short
+    warm-up alone (5 steps of 1.4 ms) leaves the first timed steps below the steady clock.
+    Nothing here is part of the timed region or changes what a step does."""
+    seconds = SETTLE_SECONDS if seconds is None else seconds
+    if seconds <= 0:
+        return
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n, spent = 1, 0.0
+    while spent < seconds * 1e3:
+        e0.record()
+        for _ in range(n):
+            for f in step_fns:
+                f()
+        e1.record()
+        torch.cuda.synchronize()
+        spent += e0.elapsed_time(e1)
+        n = min(2 * n, 256)
+
+
 def time_steps(torch, step_fns, steps, warmup):
     """Runs `steps` steps of the stage functions; returns (total ms, [ms per stage]).
 
@@ -134,6 +159,7 @@ def time_steps(torch, step_fns, steps, warmup):
     the per-stage times from a second pass with an event pair around every launch (an event
     between two kernels delays the second one's dispatch, which the first pass keeps out of
     the step time)."""
+    settle(torch, step_fns)
     for _ in range(warmup):
         for f in step_fns:
             f()
@@ -319,14 +345,16 @@ def bench_torch_sdpa(torch, t, steps, warmup):
         "ms": ms, "tflops": attn_flops(B, H, L, L) / (ms * 1e-3) / 1e12}}
 
 
-def dit_setup(torch, W, dev, layers):
-    """A `layers`-layer DiT at 704x544x81 with random bf16 weights (std 0.02), the HIP
-    attention path, both prompts' cross K/V set and one warm-up forward done."""
+def dit_setup(torch, W, dev, layers, grid=GRID_C, model=None):
+    """A `layers`-layer DiT at the token grid `grid` (704x544x81 by default) with random bf16
+    weights (std 0.02), the HIP attention path, both prompts' cross K/V set and one warm-up
+    forward done.  `model`: reuse these weights instead of drawing new ones."""
     cfg = W.model.WanConfig()
-    model = W.model.random_model(cfg, num_layers=layers, device=dev, seed=0)
-    fast = W.fast_dit.FastWanDiT(model, GRID_C, cfg.sample_guide_scale, attn_impl="hip", cross_impl="hip")
+    if model is None:
+        model = W.model.random_model(cfg, num_layers=layers, device=dev, seed=0)
+    fast = W.fast_dit.FastWanDiT(model, grid, cfg.sample_guide_scale, attn_impl="hip", cross_impl="hip")
     g = torch.Generator().manual_seed(5)
-    f, h, w = GRID_C
+    f, h, w = grid
     latent = torch.randn(cfg.in_dim, f, 2 * h, 2 * w, generator=g).to(dev)     # [48, 21, 34, 44]
     ctx_c = torch.randn(1, cfg.text_len, cfg.text_dim, generator=g).to(dev)
     ctx_n = torch.randn(1, cfg.text_len, cfg.text_dim, generator=g).to(dev)
@@ -363,7 +391,8 @@ def profile_block(torch, W, dev, steps):
 def bench_dit(torch, W, dev, steps, layers):
     """Config D (one WanAttentionBlock at L=7854) and config E (the 30-layer DiT, 10 UniPC
     steps at 704x544x81) with random bf16 weights (std 0.02) and the HIP attention path."""
-    cfg, fast, latent, image_latent = dit_setup(torch, W, dev, layers)
+    cfg = W.model.WanConfig()
+    cfg, fast, latent, image_latent = dit_setup(torch, W, dev, layers, model=fast_model(cfg, W, dev, layers))
 
     # config D: one block, its inputs as in the DiT
     blk, inputs = block_inputs(torch, fast, latent)
@@ -394,7 +423,7 @@ def bench_dit(torch, W, dev, steps, layers):
     dit_s = e_a.elapsed_time(e_b) / 1e3
     finite = bool(torch.isfinite(final.float()).all())
     step_flops = layers * block_flops
-    return {
+    res = {
         "block_D": {"workload": "one WanAttentionBlock forward, B=2, L=7854, dim 3072, ffn 14336, "
                                 "24 heads, 512 text keys, random bf16 weights",
                     "ms": block_ms, "tflops": block_flops / (block_ms * 1e-3) / 1e12},
@@ -403,6 +432,38 @@ def bench_dit(torch, W, dev, steps, layers):
                   "s_per_step": dit_s / steps, "wall_s_per_step": wall / steps,
                   "tflops": step_flops / (dit_s / steps) / 1e12, "finite": finite},
     }
+    del final, fast
+
+    # the same DiT at the reference's 368x480x21 size: generated at 384x480 (latent
+    # 48 x 6 x 24 x 30, 1080 tokens) and centre-cropped, as README.md:41 of the reference
+    _, fast_a, latent_a, image_a = dit_setup(torch, W, dev, layers, GRID_A, model=fast_model(cfg, W, dev, layers))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e_a.record()
+    final = W.fast_dit.denoise(fast_a, latent_a, steps, cfg.sample_shift, image_latent=image_a)
+    e_b.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    s_a = e_a.elapsed_time(e_b) / 1e3 / steps
+    LA = GRID_A[0] * GRID_A[1] * GRID_A[2]
+    flops_a = layers * (2.0 * B * LA * (6 * C * C + 2 * C * Fd) + attn_flops(B, H, LA, LA)
+                        + 4.0 * B * H * LA * L_TEXT * D)
+    res["dit_E_L1080"] = {
+        "workload": f"{layers}-layer Wan2.2-TI2V-5B DiT, {steps} UniPC steps, 368x480x21 generated at 384x480 "
+                    "(latent 48x6x24x30, L=1080), CFG batch 2, random bf16 weights (the same as dit_E)",
+        "s_per_step": s_a, "wall_s_per_step": wall / steps, "tflops": flops_a / s_a / 1e12,
+        "finite": bool(torch.isfinite(final.float()).all())}
+    return res
+
+
+_MODEL = {}
+
+
+def fast_model(cfg, W, dev, layers):
+    """The random-weight model of the DiT runs, drawn once per process."""
+    if layers not in _MODEL:
+        _MODEL[layers] = W.model.random_model(cfg, num_layers=layers, device=dev, seed=0)
+    return _MODEL[layers]
 
 
 def cpu_baseline(torch, hosts, seconds):
@@ -472,6 +533,8 @@ def main():
     # after idle the part raises its clocks over the first ~0.1 s of work: 100 untimed steps
     # (~0.15 s at config C) put the timed steps at the steady state
     ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--settle-seconds", type=float, default=SETTLE_SECONDS,
+                    help="untimed clock settle before each timed config's warm-up steps (0: none)")
     ap.add_argument("--cpu-seconds", type=float, default=25.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
@@ -489,6 +552,8 @@ def main():
               f"a single MI355X and has no multi-GPU path (asked for --gpus {args.gpus}).", file=sys.stderr)
         sys.exit(2)
 
+    global SETTLE_SECONDS
+    SETTLE_SECONDS = args.settle_seconds
     sys.path.insert(0, ROOT)
     import __graft_entry__
     W = __graft_entry__.load_package()
@@ -558,7 +623,8 @@ def main():
         log(f"extra: {json.dumps(extra)}")
     if not args.no_dit:
         extra.update(bench_dit(torch, W, dev, args.dit_steps, args.dit_layers))
-        log(f"block D: {extra['block_D']['ms']:.2f} ms; DiT E: {extra['dit_E']['s_per_step']:.3f} s/step")
+        log(f"block D: {extra['block_D']['ms']:.2f} ms; DiT E: {extra['dit_E']['s_per_step']:.3f} s/step "
+            f"(L=1080: {extra['dit_E_L1080']['s_per_step']:.4f} s/step)")
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -54,6 +54,15 @@ const char* wan_attn_last_error(void);
 int wan_attn_abi_version(void);
 
 /*
+ * Set-up for the current device: looks up the device address of the library's static
+ * scratch (used by wan_cross_attn_fused_noalloc) once, so that no runtime lookup happens
+ * later inside a HIP graph capture.  Idempotent; call it with each device current that
+ * will run the no-allocation entry point.  Allocates nothing.  No counterpart in the
+ * reference (its kernels have no library-owned device state).
+ */
+int wan_attn_init(void);
+
+/*
  * Self-attention, out = softmax(q k^T * softmax_scale) v over the first
  * actual_seqlen_k keys (actual_seqlen_k <= 0 means all seqlen_k keys).
  * Replaces wan_flash_self_attn, kernels/self_attention_nst.py:49-117, and the
@@ -113,8 +122,10 @@ int wan_cross_attn_fused(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor ou
  * forbid hipMalloc).  No counterpart in the reference.  The per-row inverse RMS of q goes
  * to a scratch array owned by the library: WAN_NOALLOC_MAX_ROWS fp32 rows (512 KB) per
  * GPU, held until the process ends; batch * seqlen_q above that returns
- * WAN_ERR_UNSUPPORTED.  The array's device address is looked up on the first call on
- * each device (the device current at the call).  Nothing is allocated or freed.  Every
+ * WAN_ERR_UNSUPPORTED.  The array's device address is looked up by wan_attn_init() on
+ * the device current at that call; without it, on the entry point's first call on each
+ * device.  A caller that captures the first call into a HIP graph calls wan_attn_init()
+ * on that device before the capture begins.  Nothing is allocated or freed.  Every
  * call on one GPU shares that GPU's array: calls that overlap on one GPU (e.g. on two
  * streams) race and must be ordered by the caller.  Same kernels and results as
  * wan_cross_attn_fused.

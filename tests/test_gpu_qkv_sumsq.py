@@ -8,7 +8,8 @@
   * sumsq against the sums of squares of the GEMM's own bf16 output, per 64 columns;
   * inv_rms_q and the normalised, rotated k from the sums against wan_rms_norm_qk, which
     computes them from the rows (the fp32 sum order differs: equal up to rare one-ulp flips
-    before the rotation, bounded against each rotated pair's norm);
+    before the rotation, bounded against each rotated pair's norm), and against the oracle
+    (oracle.inv_rms, oracle.rms, oracle.rope) on the GEMM's own q and k;
   * a whole WanAttentionBlock with FAST_QKV_IMPL "hip" against the default "hipblaslt".
 """
 import pytest
@@ -108,6 +109,24 @@ def test_qk_prep_from_sums(W, grid):
     ulp = pair.clamp_min(2 ** -100) * 2 ** -7
     frac = float((d > 0).float().mean())
     print(f"grid {grid}: k-hat elements differing {frac:.2e}, max {float((d / ulp).max()):.2f} ulp of the pair norm")
+    assert bool((d <= 4 * ulp).all()) and frac < 1e-2
+
+    # ... and both against the oracle on the GEMM's own q and k: the q statistic
+    # 1/sqrt(mean(q^2) + eps) (oracle.inv_rms) and k-hat = rope(rms(k) * gamma_k)
+    # (oracle.rms, oracle.rope: the reference's rounding points, models/fast_dit.py:134-169)
+    qh, kh = q.cpu().reshape(B, L, C), k.cpu().reshape(B, L, C)
+    inv_want = ref.inv_rms(qh).reshape(-1)
+    ei = float(((inv1.cpu() - inv_want).abs() / inv_want).max())
+    print(f"grid {grid}: inv_rms_q from the sums vs oracle.inv_rms: max rel {ei:.2e}")
+    assert ei <= 2e-6
+    cos_h, sin_h = ref.rope_tables(ref.wan_freqs(D), grid, D)
+    k_want = ref.rope(ref.rms(kh, gk.cpu()).view(B, L, H, D), cos_h, sin_h)
+    d = (k1.cpu().float() - k_want.float()).abs()
+    pair = k_want.float().view(B, L, H, D // 2, 2).pow(2).sum(-1).sqrt().repeat_interleave(2, -1).view(B, L, H, D)
+    ulp = pair.clamp_min(2 ** -100) * 2 ** -7
+    frac = float((d > 0).float().mean())
+    print(f"grid {grid}: k-hat from the sums vs the oracle: differing {frac:.2e}, "
+          f"max {float((d / ulp).max()):.2f} ulp of the pair norm")
     assert bool((d <= 4 * ulp).all()) and frac < 1e-2
 
 

@@ -36,7 +36,7 @@ def _sgprs(tok):
     m = re.match(r"s\[(\d+):(\d+)\]$", tok)
     if m:
         return {f"s{k}" for k in range(int(m.group(1)), int(m.group(2)) + 1)}
-    return {tok} if re.match(r"s\d+$", tok) else set()
+    return {tok} if re.match(r"(s\d+|m0)$", tok) else set()
 
 
 def instructions(asm_text):
@@ -65,6 +65,9 @@ def valu_sgpr_hazards(ins):
         srcs = set()
         for t in (toks[1:] if "load" in parts[0] else toks):
             srcs |= _sgprs(t)
+        # a global -> LDS copy also reads m0 (its LDS destination), an implicit operand
+        if "_lds_" in parts[0]:
+            srcs.add("m0")
         for r in srcs:
             for j in range(i - 1, max(-1, i - WAIT_STATES - 1), -1):
                 p = ins[j][1].split()
@@ -108,6 +111,26 @@ _Zk:
     global_load_lds_dwordx4 v185, s[8:9]
 """)
     assert not valu_sgpr_hazards(rewritten)
+    # m0 is an implicit operand of a global -> LDS copy: a VALU write of m0 counts
+    m0_valu = instructions("""
+_Zk:
+    v_readfirstlane_b32 m0, v12
+    s_nop 0
+    global_load_lds_dwordx4 v193, s[12:13]
+""")
+    assert [h[3] for h in valu_sgpr_hazards(m0_valu)] == [2]
+    m0_salu = instructions("""
+_Zk:
+    v_readfirstlane_b32 s20, v12
+    s_nop 4
+    s_nop 4
+    s_nop 4
+    s_nop 4
+    s_mov_b32 m0, s20
+    s_nop 0
+    global_load_lds_dwordx4 v193, s[12:13]
+""")
+    assert not valu_sgpr_hazards(m0_salu)
 
 
 def _sources_with_inline_memory_asm():

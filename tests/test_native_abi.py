@@ -213,8 +213,15 @@ def test_qkv_gemm_and_sumsq_prep_validation_without_launching(W):
     # strides beyond the 32-bit tile offsets
     assert gemm(P, P, P, P, P, 64, 512, 128, 1 << 23, 128, 512, 128, None) == 2
     # a missing bias, misaligned output
-    assert gemm(P, P, None, P, P, 64, 512, 128, 128, 128, 512, 128, None) == 1 and "aligned" in N.last_error()
+    assert gemm(P, P, None, P, P, 64, 512, 128, 128, 128, 512, 128, None) == 1 and "NULL" in N.last_error()
     assert gemm(P, P, P, P + 2, P, 64, 512, 128, 128, 128, 512, 128, None) == 1
+    # NULL x / w / out are refused whether or not sums of squares are asked for: with
+    # sumsq NULL and sq_cols 0 only sumsq may be missing
+    for args in ((None, P, P, P), (P, None, P, P), (P, P, P, None), (P, P, None, P)):
+        assert gemm(*args, None, 64, 512, 128, 128, 128, 512, 0, None) == 1 and "NULL" in N.last_error()
+    assert gemm(P, P, P, P, None, 64, 512, 128, 128, 128, 512, 128, None) == 1 and "sumsq" in N.last_error()
+    # every pointer may be NULL when there are no rows
+    assert gemm(None, None, None, None, None, 0, 512, 128, 128, 128, 512, 0, None) == 0
     # K = 0 is refused (no tile to accumulate); M = 0 is nothing to do
     assert gemm(P, P, P, P, P, 64, 512, 0, 128, 128, 512, 128, None) == 1 and "bad sizes" in N.last_error()
     assert gemm(P, P, P, P, P, 0, 512, 128, 128, 128, 512, 128, None) == 0

@@ -36,6 +36,7 @@ _T = WanTensor
 SIGNATURES = {
     "wan_attn_last_error": (ctypes.c_char_p, []),
     "wan_attn_abi_version": (_I, []),
+    "wan_attn_init": (_I, []),
     "wan_flash_self_attn": (_I, [_T, _T, _T, _T, _I, _I, _I, _I, _I, _F, _I, _P]),
     "wan_cross_attn": (_I, [_T, _T, _T, _T, _I, _I, _I, _I, _I, _F, _P, _P]),
     "wan_self_attn_fused_workspace": (_SZ, [_I, _I, _I]),

@@ -6,6 +6,8 @@ selector is explicit: impl "hip" (default; USE_HIP_KERNELS=1) runs the gfx950
 kernels and requires HIP tensors, raising otherwise (no silent host fallback);
 impl "sdpa" (USE_HIP_KERNELS=0) runs torch SDPA.  Unlike the reference's SDPA
 fallback, which ignores k_lens with a warning (:222-227), both honour k_lens.
+Host-side k_lens are checked against [1, Lk] as the reference's kernel_assert states;
+k_lens already on the device are not read back (no host wait): the kernels clamp them.
 """
 import os
 from typing import Optional
@@ -28,6 +30,11 @@ def attention(q, k, v, q_lens=None, k_lens: Optional[torch.Tensor] = None, dropo
     if USE_HIP_KERNELS:
         q, k, v = (t.to(dtype) for t in (q, k, v))
         if k_lens is not None:
+            if isinstance(k_lens, torch.Tensor) and k_lens.device.type == "cuda":
+                # lengths already on the device are passed as they are: reading them here
+                # would make the host wait for the stream; the kernels clamp each length
+                # to [0, Lk] and give zeros for a sample with no keys
+                return ops.cross_attn(q, k, v, k_lens.to(torch.int32), scale)
             lens = torch.as_tensor(k_lens, dtype=torch.int32)
             if int(lens.min()) < 1 or int(lens.max()) > k.shape[1]:
                 raise ValueError(f"k_lens must be in [1, {k.shape[1]}], got {lens.tolist()}")

@@ -373,7 +373,8 @@ constexpr int kMaxDevices = 64;
 float* g_scratch_dev[kMaxDevices] = {};
 std::mutex g_scratch_mu;
 
-// The current device's copy of `scratch` (looked up on the first call on that device).
+// The current device's copy of `scratch`, looked up by wan_attn_init() or on the first
+// no-allocation call on that device.
 int device_scratch(const char* fn, float** ptr) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
@@ -396,6 +397,12 @@ int device_scratch(const char* fn, float** ptr) {
 }  // namespace
 
 extern "C" {
+
+int wan_attn_init(void) {
+  float* p = nullptr;
+  (void)device_cu_count();
+  return device_scratch("wan_attn_init", &p);
+}
 
 int wan_cross_attn_fused(wan_tensor q, wan_tensor k, wan_tensor v, wan_tensor out, int batch,
                          int heads, int seqlen_q, int seqlen_k, int head_dim, const void* gamma_q,
@@ -473,9 +480,14 @@ int wan_qkv_proj_sumsq(const void* x, const void* w, const void* bias, void* out
   // a tile's 256 rows are addressed with 32-bit byte offsets
   if (ldx >= (int64_t(1) << 23) || ldw >= (int64_t(1) << 23))
     return set_error(WAN_ERR_UNSUPPORTED, "%s: row strides must be below 2^23 elements", fn);
+  // x, w, bias and out are always read or written when M > 0; sumsq only when sq_cols > 0
+  if (M > 0 && (x == nullptr || w == nullptr || bias == nullptr || out == nullptr))
+    return set_error(WAN_ERR_INVALID, "%s: x, w, bias and out must not be NULL", fn);
+  if (M > 0 && sq_cols > 0 && sumsq == nullptr)
+    return set_error(WAN_ERR_INVALID, "%s: sumsq must not be NULL when sq_cols > 0", fn);
   const void* ptrs[] = {x, w, bias, out, sumsq};
   for (const void* p : ptrs)
-    if (!aligned16(p) || (p == nullptr && !(p == sumsq && sq_cols == 0) && M > 0))
+    if (!aligned16(p))
       return set_error(WAN_ERR_INVALID, "%s: operands must be 16-byte aligned device pointers", fn);
   GemmArgs a;
   a.x = static_cast<const bf16*>(x);

@@ -114,6 +114,8 @@ struct FlashArgs {
   const float* sin;
 };
 int launch_flash_fwd(const FlashArgs& a, hipStream_t s);
+// CU count of the current device (cached per device after the first query).
+int device_cu_count();
 
 // out = bf16(x w^T + bias) with per-head sums of squares of the first sq_cols columns.
 struct GemmArgs {

@@ -906,15 +906,7 @@ template __global__ void flash_short_kernel<kQNorm>(const FlashArgs, int);
 // and odd (so that one workgroup's consecutive items alternate between the samples
 // of a batch of 2).
 int short_grid(int items) {
-  static int cus[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (cus[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cus[dev] = n;
-  }
-  int w = 2 * (cus[dev] / kNumXcd);
+  int w = 2 * (device_cu_count() / kNumXcd);
   w = w > 1 ? w - 1 : 1;
   const int need = (items + kNumXcd - 1) / kNumXcd;
   return kNumXcd * (need < w ? need : w);
@@ -967,6 +959,20 @@ int launch_qp(const FlashArgs& a, hipStream_t s) {
 }
 
 }  // namespace
+
+// CU count of the current device, queried once per device (wan_attn_init() does that
+// before any launch, so that no runtime query happens inside a graph capture).
+int device_cu_count() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
 
 int launch_flash_fwd(const FlashArgs& a, hipStream_t s) {
   if (a.B == 0 || a.H == 0 || a.Lq == 0) return 0;

@@ -146,6 +146,27 @@ def _sdpa(q, k, v, seqlen_k: Optional[Sequence[int]] = None, scale: Optional[flo
     return torch.cat([one(q[b:b + 1], k[b:b + 1, :n], v[b:b + 1, :n]) for b, n in enumerate(seqlen_k)], 0)
 
 
+def _pack_qkv(sa):
+    """One [3C, C] weight and [3C] bias for the fused q/k/v projection.  The q, k and v
+    parameters become views into them (same names, shapes and values, so state dicts still
+    load), so the weights are held once rather than twice.  Packed once per module."""
+    packed = getattr(sa, "_wan_qkv_packed", None)
+    layers = (sa.q, sa.k, sa.v)
+    if packed is not None and all(l.weight.data_ptr() == packed[0][i * l.weight.shape[0]:].data_ptr()
+                                  for i, l in enumerate(layers)):
+        return packed
+    w = torch.cat([l.weight.detach() for l in layers], 0).contiguous()
+    b = torch.cat([l.bias.detach() for l in layers], 0).contiguous()
+    off = 0
+    for l in layers:
+        n = l.weight.shape[0]
+        l.weight.data = w[off:off + n]
+        l.bias.data = b[off:off + n]
+        off += n
+    sa._wan_qkv_packed = (w, b)
+    return w, b
+
+
 class _FastBlock:
     """One WanAttentionBlock forward (the reference's _FastBlock, models/fast_dit.py:260-311)
     at TP=1, as the four stages of the module docstring."""
@@ -161,8 +182,7 @@ class _FastBlock:
         self.qkv_impl = qkv_impl
         sa = block.self_attn
         if attn_impl == "hip":
-            self.w_qkv = torch.cat([sa.q.weight, sa.k.weight, sa.v.weight], 0).contiguous()
-            self.b_qkv = torch.cat([sa.q.bias, sa.k.bias, sa.v.bias], 0).contiguous()
+            self.w_qkv, self.b_qkv = _pack_qkv(sa)
 
     def __call__(self, x, e0, cos, sin, ck, cv, seqlen_k=None):
         """x [B, L, C] bf16; e0 [1, F, 6, C] time projection; cos/sin [L, 64]; ck/cv the
