@@ -131,6 +131,11 @@ class FusedSelf:
 SETTLE_SECONDS = 0.3
 
 
+def set_settle(seconds):
+    global SETTLE_SECONDS
+    SETTLE_SECONDS = seconds
+
+
 def settle(torch, step_fns, seconds=None):
     """Untimed repetitions of the step for about `seconds` of device time before the warm-up
     steps.  After idle the part raises its clocks over the first ~0.1 s of work, so a short
@@ -552,8 +557,7 @@ def main():
               f"a single MI355X and has no multi-GPU path (asked for --gpus {args.gpus}).", file=sys.stderr)
         sys.exit(2)
 
-    global SETTLE_SECONDS
-    SETTLE_SECONDS = args.settle_seconds
+    set_settle(args.settle_seconds)
     sys.path.insert(0, ROOT)
     import __graft_entry__
     W = __graft_entry__.load_package()
