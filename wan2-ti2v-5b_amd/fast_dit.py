@@ -45,8 +45,8 @@ FAST_CROSS_IMPL = os.environ.get("FAST_CROSS_IMPL", FAST_ATTN_IMPL)
 FAST_POINTWISE_IMPL = os.environ.get("FAST_POINTWISE_IMPL", "hip")
 # The fused q/k/v projection of the "hip" self-attention: "hipblaslt" (default), or "hip", the
 # gfx950 GEMM whose epilogue emits the QK-RMSNorm sums of squares (ops.qkv_proj_sumsq), so the
-# q statistics pass disappears; it measures 0.72 ms against hipBLASLt's 0.61 ms at the
-# config C shape, more than the 19 us the pass costs, hence not the default.
+# q statistics pass disappears; it measures 0.70 ms against hipBLASLt's 0.60 ms at the
+# B=2, L=7854 shape, more than the 9-20 us the q read costs, hence not the default.
 FAST_QKV_IMPL = os.environ.get("FAST_QKV_IMPL", "hipblaslt")
 IMPLS = ("hip", "sdpa")
 for _name, _val in (("FAST_ATTN_IMPL", FAST_ATTN_IMPL), ("FAST_CROSS_IMPL", FAST_CROSS_IMPL)):
