@@ -216,6 +216,23 @@ int wan_adaln(const void* x, const void* y, void* x_out, void* h_out, int batch,
               const void* ln_weight, const void* ln_bias, float eps, void* stream);
 
 /*
+ * wan_adaln with the shift and scale rows taken from another row set, e_mod
+ * [frames, mod_rows, dim] (mod_rows in 1..6), while the gate keeps e's rows:
+ *   h_out = ln | bf16(bf16(ln * bf16(1 + e_mod[f, scale_idx])) + e_mod[f, shift_idx])
+ * One pass then ends one block and starts the next: the gated residual of block i
+ * (models/fast_dit.py:311, gate e_i[f, 5]) followed by block i+1's norm1 + _modulate
+ * (:280, rows e_{i+1}[f, 0..1]); or, after the last block, the output head's LayerNorm
+ * and modulation (models/fast_dit.py:480-505: two rows per frame, mod_rows = 2).
+ * The results are those of the two separate stages bit for bit (the residual is
+ * rounded to bf16 before its LayerNorm statistics, as when re-read).  e_mod = NULL is
+ * wan_adaln.  No counterpart of its own in the reference: it fuses two of its stages.
+ */
+int wan_adaln_ex(const void* x, const void* y, void* x_out, void* h_out, int batch, int seqlen,
+                 int dim, const void* e, int frames, int gate_idx, const void* e_mod, int mod_rows,
+                 int shift_idx, int scale_idx, const void* ln_weight, const void* ln_bias, float eps,
+                 void* stream);
+
+/*
  * The block's q/k/v projection with the statistics of the QK-RMSNorm in its epilogue:
  *   out[m, n]   = bf16(sum_k x[m, k] w[n, k] + bias[n])           (bf16, fp32 accumulation)
  *   sumsq[p, m] = sum over columns 64 p .. 64 p + 63 of bf16(out[m, n])^2,  p < sq_cols / 64

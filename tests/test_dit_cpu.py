@@ -258,3 +258,26 @@ def test_qkv_weights_are_packed_once_as_views(W):
     sd = {k: v.clone() + 1 for k, v in m.blocks[0].state_dict().items()}
     m.blocks[0].load_state_dict(sd)
     assert torch.equal(fb.w_qkv[C:2 * C], sd["self_attn.k.weight"])
+
+
+def test_chained_block_boundaries_equal_separate_stages(W):
+    """FastWanDiT does each block boundary in one pointwise call (block i's gated residual
+    with block i+1's norm1 + modulation; the last block's with the head's): with the eager
+    torch stages the guided prediction equals, bit for bit, running every block's four
+    stages and the head's own stage separately."""
+    m = _tiny(W)
+    grid = (3, 4, 5)
+    fast = W.fast_dit.FastWanDiT(m, grid, guide_scale=5.0, attn_impl="sdpa", cross_impl="sdpa",
+                                 pointwise_impl="eager")
+    g = torch.Generator().manual_seed(3)
+    latent = torch.randn(4, 3, 8, 10, generator=g)
+    ctx_c, ctx_n = torch.randn(1, 7, 64, generator=g), torch.randn(1, 7, 64, generator=g)
+    fast.set_context(ctx_c, ctx_n)
+    t = torch.tensor(600)
+    got = fast(latent, t)
+    e, e0 = fast.time_rows(t)
+    x = fast.patch(latent)
+    for blk, (ck, cv) in zip(fast.blocks, fast.context):
+        x = blk(x, e0, fast.cos, fast.sin, ck, cv, fast.seqlen_k)
+    want = W.fast_dit.noise_prediction(m.head, x, e, grid, m.patch_size, m.out_dim, 5.0)
+    assert torch.equal(got, want)

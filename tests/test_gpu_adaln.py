@@ -87,3 +87,34 @@ def test_outputs_are_layer_norm_statistics(W):
     hf = h.float()
     assert float(hf.mean(-1).abs().max()) < 2e-3
     assert float((hf.pow(2).mean(-1) - 1).abs().max()) < 1e-2
+
+
+@pytest.mark.parametrize("mod_rows,shift,scale", [(6, 0, 1), (2, 0, 1)])
+def test_boundary_stage_equals_two_stages(W, mod_rows, shift, scale):
+    """wan_adaln_ex: one block's gated residual (gate e[5]) and the following stage's
+    LayerNorm + modulation from another row set in one pass, at B=2, L=7854, 21 frames: the
+    next block's norm1 + modulate (6 rows per frame) and the output head's (2 rows).  Both
+    outputs must equal the two separate stages bit for bit (the residual is rounded to bf16
+    before its statistics, exactly as when the second stage re-reads it); h also against the
+    oracle's rounding points."""
+    B, L, C, Fr = 2, 7854, 3072, 21
+    x, y, e, _, _ = _inputs(B, L, C, Fr, 21)
+    g = torch.Generator().manual_seed(22)
+    e_mod = (torch.randn(Fr, mod_rows, C, generator=g) * 0.5).bfloat16()
+    xd, yd, ed, md = (t.to(DEV) for t in (x, y, e, e_mod))
+    r1, _ = W.ops.adaln(xd, yd, ed, Fr, gate_idx=5, norm=False)
+    e6 = md if mod_rows == 6 else torch.zeros(Fr, 6, C, dtype=torch.bfloat16, device=DEV)
+    if mod_rows != 6:
+        e6[:, :mod_rows] = md
+    _, h1 = W.ops.adaln(r1, None, e6.contiguous(), Fr, shift_idx=shift, scale_idx=scale)
+    r2, h2 = W.ops.adaln(xd, yd, ed, Fr, gate_idx=5, shift_idx=shift, scale_idx=scale, e_mod=md)
+    torch.cuda.synchronize()
+    assert torch.equal(r2, r1) and torch.equal(h2, h1)
+    # the oracle: gate + residual, then LayerNorm + modulation with the other rows
+    r_want, _ = ref.adaln(x, y, e, Fr, gate_idx=5, norm=False)
+    _, h_want = ref.adaln(r_want, None, e6.cpu(), Fr, shift_idx=shift, scale_idx=scale)
+    assert torch.equal(r2.cpu(), r_want)
+    nbad, frac = _compare_h(h2.cpu(), h_want)
+    print(f"boundary stage, {mod_rows} modulation rows: bit-identical to two stages; "
+          f"h differs from the oracle on {frac:.2e} of elements")
+    assert nbad == 0 and frac <= 1e-2

@@ -172,3 +172,34 @@ def test_ffn_gelu_epilogue_is_tanh_form(W):
     d_erf = float((y - F.gelu(xs)).abs().max())
     print(f"gelu epilogue: max diff vs tanh {d_tanh:.2e}, vs erf {d_erf:.2e}")
     assert d_tanh < 1e-5 < d_erf
+
+
+@pytest.mark.parametrize("dim,heads,layers", [(256, 2, 3), (3072, 24, 2)])
+def test_chained_block_boundaries_bit_identical(W, dim, heads, layers):
+    """FastWanDiT ends each block with one fused pass that also makes the next block's norm1
+    + modulation (and, after the last block, the head's): the guided prediction equals, bit
+    for bit, every block's four separate stages followed by the head's own stage, with the
+    HIP attention and pointwise kernels (the full-width case at a short grid)."""
+    cfg = W.model.WanConfig(**dict(TINY, dim=dim, num_heads=heads, num_layers=layers,
+                                   ffn_dim=4 * dim))
+    m = W.model.random_model(cfg, device=DEV, std=0.05, seed=4)
+    grid = (3, 4, 5)
+    g = torch.Generator().manual_seed(5)
+    latent = torch.randn(4, 3, 8, 10, generator=g).to(DEV)
+    ctx_c, ctx_n = (torch.randn(1, 7, 64, generator=g).to(DEV) for _ in range(2))
+    fast = W.fast_dit.FastWanDiT(m, grid, 5.0, attn_impl="hip", cross_impl="hip", pointwise_impl="hip")
+    fast.set_context(ctx_c, ctx_n)
+    t = torch.tensor(650)
+    got = fast(latent, t)
+    e, e0 = fast.time_rows(t)
+    x = fast.patch(latent)
+    for blk, (ck, cv) in zip(fast.blocks, fast.context):
+        x = blk(x, e0, fast.cos, fast.sin, ck, cv, fast.seqlen_k)
+    # the head's LayerNorm + modulation as its own pass of the same kernel (torch's LayerNorm
+    # may order its fp32 sums differently and flip a bf16 rounding)
+    rows = W.fast_dit.head_rows(m.head, e, grid[0])
+    _, h = W.ops.adaln(x, None, None, grid[0], shift_idx=0, scale_idx=1, eps=m.head.norm.eps, e_mod=rows)
+    want = W.fast_dit.noise_prediction(m.head, x, e, grid, m.patch_size, m.out_dim, 5.0, h=h)
+    torch.cuda.synchronize()
+    print(f"chained DiT dim={dim} layers={layers}: bit-identical {torch.equal(got, want)}")
+    assert torch.isfinite(got.float()).all() and torch.equal(got, want)

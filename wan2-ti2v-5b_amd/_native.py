@@ -49,6 +49,7 @@ SIGNATURES = {
     "wan_rms_norm_qk": (_I, [_T, _T, _P, _I, _I, _I, _I, _P, _F, _P, _P, _P, _P]),
     "wan_flash_attn_qnorm": (_I, [_T, _T, _T, _T, _I, _I, _I, _I, _I, _P, _P, _P, _P, _F, _P, _P]),
     "wan_adaln": (_I, [_P, _P, _P, _P, _I, _I, _I, _P, _I, _I, _I, _I, _P, _P, _F, _P]),
+    "wan_adaln_ex": (_I, [_P, _P, _P, _P, _I, _I, _I, _P, _I, _I, _P, _I, _I, _I, _P, _P, _F, _P]),
     "wan_qkv_proj_sumsq": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _L, _L, _L, _I, _P]),
     "wan_rms_norm_qk_sumsq": (_I, [_T, _P, _I, _I, _I, _I, _P, _F, _P, _P, _P, _P, _P]),
 }

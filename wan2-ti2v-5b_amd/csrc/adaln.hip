@@ -7,7 +7,11 @@
 //   ln = bf16(LayerNorm(r))        fp32 mean / biased variance over the dim channels,
 //                                  [* w + b] when the norm is affine
 //   h = ln                         (no modulation)
-//   h = bf16(bf16(ln * bf16(1 + e[f, scale_idx])) + e[f, shift_idx])
+//   h = bf16(bf16(ln * bf16(1 + m[f, scale_idx])) + m[f, shift_idx])
+//
+// The modulation rows m are e itself, or another row set: the next block's rows when
+// one pass ends a block (gated residual) and starts the next (norm1 + modulate), or
+// the output head's two rows per frame after the last block.
 //
 // f is the frame of the token (tokens of one frame are contiguous).  The
 // rounding points are those of the reference's eager bf16 graph:
@@ -19,7 +23,7 @@
 //
 // Memory bound: one wave per token row, each lane holding dim/64 channels in
 // registers between the statistics and the output; 16-byte loads and stores.
-#include "common.h"
+#include "launchers.h"
 
 namespace wan {
 
@@ -39,6 +43,7 @@ __global__ __launch_bounds__(256) void adaln_kernel(const AdaLNArgs a) {
   const int C = a.C, nch = C >> 3;
   const int64_t row = tok * C;
   const bf16* erow = a.e + (int64_t)f * 6 * C;
+  const bf16* mrow = a.e_mod + (int64_t)f * a.mod_rows * C;
 
   float r[NCH][8];
   float sum = 0.f;
@@ -101,8 +106,8 @@ __global__ __launch_bounds__(256) void adaln_kernel(const AdaLNArgs a) {
       }
       bf16x8 hv;
       if (a.shift_idx >= 0) {
-        const bf16x8 sh = *reinterpret_cast<const bf16x8*>(erow + a.shift_idx * C + 8 * c);
-        const bf16x8 sc = *reinterpret_cast<const bf16x8*>(erow + a.scale_idx * C + 8 * c);
+        const bf16x8 sh = *reinterpret_cast<const bf16x8*>(mrow + a.shift_idx * C + 8 * c);
+        const bf16x8 sc = *reinterpret_cast<const bf16x8*>(mrow + a.scale_idx * C + 8 * c);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const bf16 ln = (bf16)v[j];

@@ -9,7 +9,7 @@
 #include <mutex>
 
 #include "../../include/wan_attn.h"
-#include "common.h"
+#include "launchers.h"
 
 namespace wan {
 
@@ -505,10 +505,11 @@ int wan_qkv_proj_sumsq(const void* x, const void* w, const void* bias, void* out
   return launch_gemm_rowsq(a, static_cast<hipStream_t>(stream));
 }
 
-int wan_adaln(const void* x, const void* y, void* x_out, void* h_out, int batch, int seqlen,
-              int dim, const void* e, int frames, int gate_idx, int shift_idx, int scale_idx,
-              const void* ln_weight, const void* ln_bias, float eps, void* stream) {
-  const char* fn = "wan_adaln";
+int wan_adaln_ex(const void* x, const void* y, void* x_out, void* h_out, int batch, int seqlen,
+                 int dim, const void* e, int frames, int gate_idx, const void* e_mod, int mod_rows,
+                 int shift_idx, int scale_idx, const void* ln_weight, const void* ln_bias, float eps,
+                 void* stream) {
+  const char* fn = e_mod ? "wan_adaln_ex" : "wan_adaln";
   if (batch < 0 || seqlen < 0 || dim <= 0 || frames <= 0)
     return set_error(WAN_ERR_INVALID, "%s: bad sizes (batch=%d seqlen=%d dim=%d frames=%d)", fn,
                      batch, seqlen, dim, frames);
@@ -517,19 +518,25 @@ int wan_adaln(const void* x, const void* y, void* x_out, void* h_out, int batch,
   if (seqlen % frames != 0)
     return set_error(WAN_ERR_INVALID, "%s: seqlen=%d is not a multiple of frames=%d", fn, seqlen,
                      frames);
-  if (gate_idx < -1 || gate_idx > 5 || shift_idx < -1 || shift_idx > 5 || scale_idx < -1 ||
-      scale_idx > 5 || ((shift_idx < 0) != (scale_idx < 0)))
+  if (e_mod == nullptr) {
+    e_mod = e;
+    mod_rows = 6;
+  } else if (mod_rows < 1 || mod_rows > 6) {
+    return set_error(WAN_ERR_INVALID, "%s: mod_rows=%d must be in [1, 6]", fn, mod_rows);
+  }
+  if (gate_idx < -1 || gate_idx > 5 || shift_idx < -1 || shift_idx >= mod_rows || scale_idx < -1 ||
+      scale_idx >= mod_rows || ((shift_idx < 0) != (scale_idx < 0)))
     return set_error(WAN_ERR_INVALID, "%s: modulation rows gate=%d shift=%d scale=%d out of range",
                      fn, gate_idx, shift_idx, scale_idx);
   if (x == nullptr || (y == nullptr && x_out != nullptr) || (gate_idx >= 0 && y == nullptr))
     return set_error(WAN_ERR_INVALID, "%s: x is NULL, or x_out / a gate given without y", fn);
   if (h_out == nullptr && (shift_idx >= 0 || ln_weight != nullptr))
     return set_error(WAN_ERR_INVALID, "%s: modulation or LayerNorm weights given without h_out", fn);
-  if ((gate_idx >= 0 || shift_idx >= 0) && e == nullptr)
+  if ((gate_idx >= 0 && e == nullptr) || (shift_idx >= 0 && e_mod == nullptr))
     return set_error(WAN_ERR_INVALID, "%s: modulation rows requested but e is NULL", fn);
   if ((ln_weight == nullptr) != (ln_bias == nullptr))
     return set_error(WAN_ERR_INVALID, "%s: LayerNorm weight and bias must be given together", fn);
-  const void* ptrs[] = {x, y, x_out, h_out, e, ln_weight, ln_bias};
+  const void* ptrs[] = {x, y, x_out, h_out, e, e_mod, ln_weight, ln_bias};
   for (const void* p : ptrs)
     if (!aligned16(p)) return set_error(WAN_ERR_INVALID, "%s: operands must be 16-byte aligned", fn);
   AdaLNArgs a;
@@ -543,12 +550,21 @@ int wan_adaln(const void* x, const void* y, void* x_out, void* h_out, int batch,
   a.F = frames;
   a.e = static_cast<const bf16*>(e);
   a.gate_idx = gate_idx;
+  a.e_mod = static_cast<const bf16*>(e_mod);
+  a.mod_rows = mod_rows;
   a.shift_idx = shift_idx;
   a.scale_idx = scale_idx;
   a.ln_w = static_cast<const bf16*>(ln_weight);
   a.ln_b = static_cast<const bf16*>(ln_bias);
   a.eps = eps;
   return launch_adaln(a, static_cast<hipStream_t>(stream));
+}
+
+int wan_adaln(const void* x, const void* y, void* x_out, void* h_out, int batch, int seqlen,
+              int dim, const void* e, int frames, int gate_idx, int shift_idx, int scale_idx,
+              const void* ln_weight, const void* ln_bias, float eps, void* stream) {
+  return wan_adaln_ex(x, y, x_out, h_out, batch, seqlen, dim, e, frames, gate_idx, nullptr, 6,
+                      shift_idx, scale_idx, ln_weight, ln_bias, eps, stream);
 }
 
 }  // extern "C"

@@ -29,7 +29,7 @@
 // ~13% slower per tile than hipBLASLt's.  4 waves of 128 x 128 (a third less LDS read
 // traffic, one wave per SIMD) run the loop at a higher clock (1.72 vs 1.58 GHz) but in
 // more cycles per tile, and tie with this tiling at best.
-#include "common.h"
+#include "launchers.h"
 
 #include <type_traits>
 

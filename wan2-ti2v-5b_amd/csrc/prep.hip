@@ -7,7 +7,7 @@
 //   _rope       models/fast_dit.py:163-169   fp32 pair rotation of u, one bf16 rounding
 // Contraction into FMAs is disabled in the rotation so each product and sum is
 // rounded as the separate torch ops round it.
-#include "common.h"
+#include "launchers.h"
 
 namespace wan {
 

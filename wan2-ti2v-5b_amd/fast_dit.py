@@ -89,34 +89,38 @@ def _by_frame(t, num_frames):
     return t.unflatten(1, (num_frames, t.shape[1] // num_frames))
 
 
-def _eager_stage(x, y, e, num_frames, gate=-1, shift=-1, scale=-1, ln=None, norm=True):
+def _eager_stage(x, y, e, num_frames, gate=-1, shift=-1, scale=-1, ln=None, norm=True, mod=None):
     """One pointwise stage as separate torch ops (models/fast_dit.py:172-181,280,294,306-311);
     the same contract as ops.adaln.  e: [F, n, C] rows; returns (r, h):
         r = x, x + y, or x + y * e[gate]            (product and sum each rounded)
-        h = ln(r), then h * (1 + e[scale]) + e[shift] per frame   (None when norm is False)"""
-    def row(i):
-        return e[:, i].unsqueeze(1)                  # [F, 1, C] against [B, F, L/F, C]
+        h = ln(r), then h * (1 + m[scale]) + m[shift] per frame   (None when norm is False)
+    with m = e, or `mod` [F, n', C] when the modulation belongs to the stage that follows
+    (the next block's norm1, or the output head)."""
+    m = e if mod is None else mod
+
+    def row(t, i):
+        return t[:, i].unsqueeze(1)                  # [F, 1, C] against [B, F, L/F, C]
     r = x
     if y is not None:
         if gate >= 0:
-            y = (_by_frame(y, num_frames) * row(gate)).flatten(1, 2)
+            y = (_by_frame(y, num_frames) * row(e, gate)).flatten(1, 2)
         r = x + y
     if not norm:
         return r, None
     h = ln(r)
     if shift >= 0:
-        h = (_by_frame(h, num_frames) * (1 + row(scale)) + row(shift)).flatten(1, 2)
+        h = (_by_frame(h, num_frames) * (1 + row(m, scale)) + row(m, shift)).flatten(1, 2)
     return r, h
 
 
-def _hip_stage(x, y, e, num_frames, gate=-1, shift=-1, scale=-1, ln=None, norm=True):
-    """The same stage as one fused pass over the residual stream (wan_adaln)."""
+def _hip_stage(x, y, e, num_frames, gate=-1, shift=-1, scale=-1, ln=None, norm=True, mod=None):
+    """The same stage as one fused pass over the residual stream (wan_adaln / wan_adaln_ex)."""
     w = b = None
     if ln is not None and ln.weight is not None:
         w, b = ln.weight, ln.bias
     eps = ln.eps if ln is not None else 1e-6
     return ops.adaln(x, y, e, num_frames, gate_idx=gate, shift_idx=shift, scale_idx=scale,
-                     ln_weight=w, ln_bias=b, eps=eps, norm=norm)
+                     ln_weight=w, ln_bias=b, eps=eps, norm=norm, e_mod=mod)
 
 
 def _ffn_eager(h, ffn):
@@ -184,24 +188,40 @@ class _FastBlock:
         if attn_impl == "hip":
             self.w_qkv, self.b_qkv = _pack_qkv(sa)
 
-    def __call__(self, x, e0, cos, sin, ck, cv, seqlen_k=None):
+    def rows(self, e0):
+        """The block's modulation rows per frame, [F, 6, C]: its modulation parameter plus the
+        time projection e0 [1, F, 6, C] (models/fast_dit.py:275-276)."""
+        blk = self.block
+        return (blk.modulation.unsqueeze(0) + e0).reshape(self.num_frames, 6, blk.modulation.shape[-1])
+
+    def __call__(self, x, e0, cos, sin, ck, cv, seqlen_k=None, h=None, next_stage=None):
         """x [B, L, C] bf16; e0 [1, F, 6, C] time projection; cos/sin [L, 64]; ck/cv the
-        block's text keys/values [B, Lc, n, d]; seqlen_k: per-sample text lengths or None."""
+        block's text keys/values [B, Lc, n, d]; seqlen_k: per-sample text lengths or None.
+
+        Chained use (FastWanDiT): h is this block's norm1 + modulation output when the pass
+        that ended the previous block already made it; next_stage = (rows, LayerNorm, shift,
+        scale) of the stage that follows this block (the next block's norm1 + modulation, or
+        the output head's), done in the same pass as this block's gated residual.  Then the
+        call returns (x, h_next); otherwise x."""
         blk, nf = self.block, self.num_frames
         B, L, C = x.shape
         fused = self.pointwise_impl == "hip" and x.is_cuda
         stage = _hip_stage if fused else _eager_stage
-        e = (blk.modulation.unsqueeze(0) + e0).reshape(nf, 6, C)
+        e = self.rows(e0)
         if fused:
             x = x.contiguous()
-        _, h = stage(x, None, e, nf, shift=0, scale=1, ln=blk.norm1)
+        if h is None:
+            _, h = stage(x, None, e, nf, shift=0, scale=1, ln=blk.norm1)
         y = _linear(self._self_attention(h, cos, sin).reshape(B, L, C), blk.self_attn.o)
         x, h = stage(x, y, e, nf, gate=2, ln=blk.norm3)
         y = _linear(self._cross_attention(h, ck, cv, seqlen_k).reshape(B, L, C), blk.cross_attn.o)
         x, h = stage(x, y, e, nf, shift=3, scale=4, ln=blk.norm2)
         y = (_ffn_gelu_epilogue if fused else _ffn_eager)(h, blk.ffn)
-        x, _ = stage(x, y, e, nf, gate=5, norm=False)
-        return x
+        if next_stage is None:
+            x, _ = stage(x, y, e, nf, gate=5, norm=False)
+            return x
+        mod, ln, shift, scale = next_stage
+        return stage(x, y, e, nf, gate=5, shift=shift, scale=scale, ln=ln, mod=mod)
 
     def _self_attention(self, h, cos, sin):
         sa = self.block.self_attn
@@ -258,17 +278,24 @@ class _FastCrossKV:
         return cross_kv(self.block, context, self.cross_impl)
 
 
-def noise_prediction(head, x, e, grid, patch_size, out_dim, guide_scale):
+def head_rows(head, e, frames):
+    """The output head's modulation rows per frame, [F, 2, C] (shift, scale): its modulation
+    parameter plus the time embedding e [1, F, C] (models/fast_dit.py:480-505)."""
+    C = head.modulation.shape[-1]
+    return (head.modulation.unsqueeze(0) + e.unsqueeze(2)).reshape(frames, 2, C)
+
+
+def noise_prediction(head, x, e, grid, patch_size, out_dim, guide_scale, h=None):
     """Output head and CFG (the reference's _FastHead, models/fast_dit.py:480-505): the final
     tokens x [2, L, C] get the head's per-frame adaLN (modulation rows from the time
     embedding e [1, F, C]) and its projection to one patch of out_dim channels each; the
     patches go back to the latent grid [2, out_dim, F*pt, H*ph, W*pw]; batch row 0 is the
-    cond and row 1 the uncond prediction, returned as uncond + guide (cond - uncond)."""
+    cond and row 1 the uncond prediction, returned as uncond + guide (cond - uncond).
+    h: the head's adaLN output when the last block's final pass already made it."""
     f, hh, ww = grid
     pt, ph, pw = patch_size
-    C = x.shape[-1]
-    rows = (head.modulation.unsqueeze(0) + e.unsqueeze(2)).reshape(f, 2, C)   # shift, scale
-    _, h = _eager_stage(x, None, rows, f, shift=0, scale=1, ln=head.norm)
+    if h is None:
+        _, h = _eager_stage(x, None, head_rows(head, e, f), f, shift=0, scale=1, ln=head.norm)
     y = _linear(h, head.head)
     n = y.shape[0]
     # token (t, i, j) patch (a, b, c) channel o -> latent [o, t*pt + a, i*ph + b, j*pw + c]
@@ -339,14 +366,25 @@ class FastWanDiT:
         return x.unsqueeze(0).expand(2, -1, -1).contiguous()
 
     def __call__(self, latent, t):
+        """One guided flow prediction.  The blocks are chained: the pass that ends block i
+        (its gated residual) also makes block i+1's norm1 + modulation, and the last block's
+        the output head's LayerNorm + modulation, so each block boundary is one pass over the
+        residual stream instead of two (the same ops and roundings as separate stages)."""
         if self.context is None:
             raise RuntimeError("FastWanDiT: call set_context() before the first step")
         e, e0 = self.time_rows(t)
         x = self.patch(latent)
-        for blk, (ck, cv) in zip(self.blocks, self.context):
-            x = blk(x, e0, self.cos, self.sin, ck, cv, self.seqlen_k)
         m = self.model
-        return noise_prediction(m.head, x, e, self.grid, m.patch_size, m.out_dim, self.guide_scale)
+        n = len(self.blocks)
+        h = None
+        for i, (blk, (ck, cv)) in enumerate(zip(self.blocks, self.context)):
+            if i + 1 < n:
+                nxt = self.blocks[i + 1]
+                following = (nxt.rows(e0), nxt.block.norm1, 0, 1)
+            else:
+                following = (head_rows(m.head, e, self.num_frames), m.head.norm, 0, 1)
+            x, h = blk(x, e0, self.cos, self.sin, ck, cv, self.seqlen_k, h=h, next_stage=following)
+        return noise_prediction(m.head, x, e, self.grid, m.patch_size, m.out_dim, self.guide_scale, h=h)
 
 
 def denoise(fast: FastWanDiT, latent: torch.Tensor, steps: int, shift: float,

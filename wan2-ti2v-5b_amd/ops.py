@@ -295,7 +295,8 @@ def _check_rows(fn: str, name: str, t: torch.Tensor, shape, device) -> None:
 @torch.library.custom_op("wan_hip::adaln", mutates_args=())
 def adaln_stage(x: torch.Tensor, y: Optional[torch.Tensor], e: Optional[torch.Tensor], frames: int,
                 gate_idx: int, shift_idx: int, scale_idx: int, ln_weight: Optional[torch.Tensor],
-                ln_bias: Optional[torch.Tensor], eps: float, norm: bool) -> Tuple[torch.Tensor, torch.Tensor]:
+                ln_bias: Optional[torch.Tensor], eps: float, norm: bool,
+                e_mod: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """One fused adaLN stage (see adaln()).  Returns (x_out, h); x_out is empty when y is
     None and h is empty when norm is False."""
     fn = "adaln"
@@ -309,6 +310,12 @@ def adaln_stage(x: torch.Tensor, y: Optional[torch.Tensor], e: Optional[torch.Te
         _check_rows(fn, "y", y, (B, L, C), x.device)
     if e is not None:
         _check_rows(fn, "e", e, (frames, 6, C), x.device)
+    mod_rows = 6
+    if e_mod is not None:
+        if e_mod.dim() != 3 or not 1 <= e_mod.shape[1] <= 6:
+            raise ValueError(f"{fn}: e_mod must be [frames, rows <= 6, C], got {tuple(e_mod.shape)}")
+        mod_rows = e_mod.shape[1]
+        _check_rows(fn, "e_mod", e_mod, (frames, mod_rows, C), x.device)
     if ln_weight is not None or ln_bias is not None:
         if ln_weight is None or ln_bias is None:
             raise ValueError(f"{fn}: give the LayerNorm weight and bias together")
@@ -317,18 +324,18 @@ def adaln_stage(x: torch.Tensor, y: Optional[torch.Tensor], e: Optional[torch.Te
     x_out = torch.empty_like(x) if y is not None else x.new_empty((0,))
     h = torch.empty_like(x) if norm else x.new_empty((0,))
     with torch.cuda.device(x.device):
-        N.check("wan_adaln", N.lib().wan_adaln(
+        N.check("wan_adaln_ex", N.lib().wan_adaln_ex(
             x.data_ptr(), None if y is None else y.data_ptr(),
             None if y is None else x_out.data_ptr(), h.data_ptr() if norm else None,
             B, L, C, None if e is None else e.data_ptr(), int(frames), int(gate_idx),
-            int(shift_idx), int(scale_idx),
+            None if e_mod is None else e_mod.data_ptr(), mod_rows, int(shift_idx), int(scale_idx),
             None if ln_weight is None else ln_weight.data_ptr(),
             None if ln_bias is None else ln_bias.data_ptr(), float(eps), _stream(x.device)))
     return x_out, h
 
 
 @adaln_stage.register_fake
-def _(x, y, e, frames, gate_idx, shift_idx, scale_idx, ln_weight, ln_bias, eps, norm):
+def _(x, y, e, frames, gate_idx, shift_idx, scale_idx, ln_weight, ln_bias, eps, norm, e_mod=None):
     x_out = x.new_empty(x.shape) if y is not None else x.new_empty((0,))
     h = x.new_empty(x.shape) if norm else x.new_empty((0,))
     return x_out, h
@@ -337,15 +344,18 @@ def _(x, y, e, frames, gate_idx, shift_idx, scale_idx, ln_weight, ln_bias, eps, 
 def adaln(x: torch.Tensor, y: Optional[torch.Tensor] = None, e: Optional[torch.Tensor] = None,
           frames: int = 1, gate_idx: int = -1, shift_idx: int = -1, scale_idx: int = -1,
           ln_weight: Optional[torch.Tensor] = None, ln_bias: Optional[torch.Tensor] = None,
-          eps: float = 1e-6, norm: bool = True):
+          eps: float = 1e-6, norm: bool = True, e_mod: Optional[torch.Tensor] = None):
     """The pointwise work of one WanAttentionBlock stage (models/fast_dit.py:280,294,306-311),
     on x [B, L, C] bf16 with the block's modulation rows e [frames, 6, C]:
 
         r = x  |  bf16(x + y)  |  bf16(x + bf16(y * e[f, gate_idx]))
-        h = bf16(LayerNorm(r) [* w + b])  [then bf16(bf16(h * bf16(1 + e[f, scale_idx])) + e[f, shift_idx])]
+        h = bf16(LayerNorm(r) [* w + b])  [then bf16(bf16(h * bf16(1 + m[f, scale_idx])) + m[f, shift_idx])]
 
-    Returns (r, h); h is None when norm is False."""
-    r, h = adaln_stage(x, y, e, frames, gate_idx, shift_idx, scale_idx, ln_weight, ln_bias, eps, norm)
+    with m = e, or e_mod [frames, rows, C] when the shift and scale belong to another row set
+    (the next block's, or the output head's two rows).  Returns (r, h); h is None when norm
+    is False."""
+    r, h = adaln_stage(x, y, e, frames, gate_idx, shift_idx, scale_idx, ln_weight, ln_bias, eps, norm,
+                       e_mod)
     return (x if y is None else r), (h if norm else None)
 
 
