@@ -147,6 +147,18 @@ def test_adaln_validation_without_launching(W):
     assert lib.wan_adaln(P, P, P, None, 1, 4, 64, P, 1, -1, 0, 1, None, None, 1e-6, None) == 1
     # nothing to do is not an error
     assert lib.wan_adaln(P, None, None, P, 0, 4, 64, None, 1, -1, -1, -1, None, None, 1e-6, None) == 0
+    # wan_adaln_ex: a second row set of 1..6 rows per frame, shift/scale indices within it,
+    # the gate still indexing e's six rows
+    ex = lib.wan_adaln_ex
+    for rows in (0, 7):
+        rc = ex(P, P, P, P, 1, 4, 64, P, 1, 5, P, rows, 0, 1, None, None, 1e-6, None)
+        assert rc == 1 and "mod_rows" in N.last_error()
+    rc = ex(P, P, P, P, 1, 4, 64, P, 1, 5, P, 2, 2, 1, None, None, 1e-6, None)
+    assert rc == 1 and "out of range" in N.last_error()
+    assert ex(P, P, P, P, 1, 4, 64, P, 1, 6, P, 2, 0, 1, None, None, 1e-6, None) == 1
+    assert ex(P, P, P, P, 1, 4, 64, P, 1, 5, P + 4, 2, 0, 1, None, None, 1e-6, None) == 1
+    # a NULL second row set is wan_adaln (six rows of e), so index 5 is in range there
+    assert ex(P, P, P, P, 0, 4, 64, P, 1, 5, None, 0, 4, 5, None, None, 1e-6, None) == 0
 
 
 def test_adaln_op_validates_on_cpu(W):
@@ -155,6 +167,9 @@ def test_adaln_op_validates_on_cpu(W):
         W.ops.adaln(x)
     xm = torch.empty(2, 12, 64, dtype=torch.bfloat16, device="meta")
     r, h = torch.ops.wan_hip.adaln(xm, xm, None, 3, -1, -1, -1, None, None, 1e-6, True)
+    assert r.shape == xm.shape and h.shape == xm.shape
+    em = torch.empty(3, 2, 64, dtype=torch.bfloat16, device="meta")
+    r, h = torch.ops.wan_hip.adaln(xm, xm, None, 3, -1, 0, 1, None, None, 1e-6, True, em)
     assert r.shape == xm.shape and h.shape == xm.shape
 
 
